@@ -1,0 +1,495 @@
+// C ABI of the DiZO ZO-step library (declared in include/dizo_amd.h).
+//
+// Responsibilities: argument validation, the host-side chunk lists of each
+// parameter table, per-device quantile tables, and error reporting. Every
+// kernel launch is preceded by checks that the table belongs to the current
+// device and that all registered ranges lie inside their allocations.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/dizo_amd.h"
+#include "dz_common.h"
+#include "dz_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int32_t fail(int32_t code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int32_t hip_fail(hipError_t e, const char* what) {
+  return fail(DZ_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int elem_size(int32_t dtype) { return dtype == DZ_DTYPE_F32 ? 4 : 2; }
+
+bool valid_dtype(int32_t dtype) {
+  return dtype == DZ_DTYPE_F32 || dtype == DZ_DTYPE_F16 || dtype == DZ_DTYPE_BF16;
+}
+
+// ---------------------------------------------------------------------------
+// Quantile table: Q[i] = RNE_T(Phi^{-1}(1/2 + (i + 1/2)/65536)), i < 32768.
+// ---------------------------------------------------------------------------
+
+// x > 0 with Phi(x) = 1/2 + r, 0 < r < 1/2, to about one double ulp. Newton
+// iterations on the well-conditioned form of Phi(x) - 1/2 - r: 0.5*erf(x/sqrt2) - r
+// near the centre, (1/2 - r) - 0.5*erfc(x/sqrt2) in the tail.
+double inv_normal_half(double r) {
+  const double q = 0.5 - r;
+  double x;
+  if (r < 0.25) {
+    x = r * 2.5066282746310002;  // r * sqrt(2 pi): Phi'(0) = 1/sqrt(2 pi)
+  } else {
+    // Abramowitz & Stegun 26.2.23 rational approximation (|error| < 4.5e-4).
+    const double t = sqrt(-2.0 * log(q));
+    x = t - (2.515517 + t * (0.802853 + t * 0.010328)) /
+                (1.0 + t * (1.432788 + t * (0.189269 + t * 0.001308)));
+  }
+  for (int it = 0; it < 12; ++it) {
+    const double g = (r < 0.25) ? 0.5 * erf(x * M_SQRT1_2) - r : q - 0.5 * erfc(x * M_SQRT1_2);
+    const double phi = exp(-0.5 * x * x) * 0.39894228040143267794;  // 1/sqrt(2 pi)
+    const double dx = g / phi;
+    x -= dx;
+    if (fabs(dx) <= 1e-17 * x) break;
+  }
+  return x;
+}
+
+// Round a positive finite double to a binary format with p significand bits
+// and minimum normal exponent emin (round to nearest, ties to even).
+double round_format(double x, int p, int emin) {
+  int e2;
+  frexp(x, &e2);  // x = m * 2^e2, m in [0.5, 1)
+  int E = e2 - 1;
+  if (E < emin) E = emin;
+  const double quantum = ldexp(1.0, E - (p - 1));
+  return nearbyint(x / quantum) * quantum;
+}
+
+uint16_t f16_bits_of_exact(double v) {  // v > 0, exactly representable in fp16
+  if (v < ldexp(1.0, -14)) return (uint16_t)(v / ldexp(1.0, -24));
+  int e2;
+  frexp(v, &e2);
+  const int E = e2 - 1;
+  const uint32_t mant = (uint32_t)(v / ldexp(1.0, E - 10)) - 1024u;
+  return (uint16_t)(((uint32_t)(E + 15) << 10) | mant);
+}
+
+struct HostTables {
+  uint32_t f32[kDzTabEntries];
+  uint16_t f16[kDzTabEntries];
+  uint16_t bf16[kDzTabEntries];
+};
+
+const HostTables& host_tables() {
+  static HostTables t;
+  static std::once_flag once;
+  std::call_once(once, [] {
+    for (int i = 0; i < kDzTabEntries; ++i) {
+      const double r = ((double)i + 0.5) / 65536.0;
+      const double x = inv_normal_half(r);
+      const float f32 = (float)round_format(x, 24, -126);
+      uint32_t u;
+      memcpy(&u, &f32, 4);
+      t.f32[i] = u;
+      t.f16[i] = f16_bits_of_exact(round_format(x, 11, -14));
+      const float bf = (float)round_format(x, 8, -126);
+      memcpy(&u, &bf, 4);
+      t.bf16[i] = (uint16_t)(u >> 16);
+    }
+  });
+  return t;
+}
+
+const void* host_table_ptr(int32_t dtype) {
+  const HostTables& t = host_tables();
+  if (dtype == DZ_DTYPE_F32) return t.f32;
+  if (dtype == DZ_DTYPE_F16) return t.f16;
+  return t.bf16;
+}
+
+// ---------------------------------------------------------------------------
+// Per-device state: quantile tables in device memory and the CU count.
+// ---------------------------------------------------------------------------
+constexpr int kMaxDevices = 64;
+
+struct DeviceState {
+  bool ready = false;
+  void* tab[3] = {nullptr, nullptr, nullptr};
+  int cus = 0;
+};
+
+std::mutex g_dev_mu;
+DeviceState g_dev[kMaxDevices];
+
+int32_t current_device(int* dev) {
+  hipError_t e = hipGetDevice(dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (*dev < 0 || *dev >= kMaxDevices) return fail(DZ_ERR_DEVICE, "device index out of range");
+  return DZ_OK;
+}
+
+// Must be called with `dev` current.
+int32_t ensure_device(int dev, DeviceState** out) {
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  DeviceState& s = g_dev[dev];
+  if (!s.ready) {
+    hipError_t e = hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
+    for (int d = 0; d < 3; ++d) {
+      const size_t bytes = (size_t)kDzTabEntries * (size_t)elem_size(d);
+      e = hipMalloc(&s.tab[d], bytes);
+      if (e != hipSuccess) return hip_fail(e, "hipMalloc(quantile table)");
+      e = hipMemcpy(s.tab[d], host_table_ptr(d), bytes, hipMemcpyHostToDevice);
+      if (e != hipSuccess) return hip_fail(e, "hipMemcpy(quantile table)");
+    }
+    s.ready = true;
+  }
+  *out = &s;
+  return DZ_OK;
+}
+
+// Checks [p, p + bytes) lies inside one device allocation.
+int32_t check_range(uint64_t p, uint64_t bytes, const char* what, int32_t i) {
+  if (p == 0) return fail(DZ_ERR_INVALID, std::string(what) + " pointer is NULL (tensor " + std::to_string(i) + ")");
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  hipError_t e = hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)(uintptr_t)p);
+  if (e != hipSuccess) {
+    return fail(DZ_ERR_RANGE, std::string(what) + " of tensor " + std::to_string(i) +
+                                  " is not device memory: " + hipGetErrorString(e));
+  }
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  if (p < b || p + bytes > b + (uint64_t)size) {
+    return fail(DZ_ERR_RANGE, std::string(what) + " range of tensor " + std::to_string(i) +
+                                  " exceeds its allocation");
+  }
+  return DZ_OK;
+}
+
+}  // namespace
+
+struct dz_table {
+  int device = -1;
+  int32_t dtype = 0;
+  bool projection = false;
+  int32_t n = 0;
+  uint32_t chunk_elems = 0;
+  uint32_t nchunks = 0;
+  std::vector<uint64_t> ptrs, aux, zoff;
+  std::vector<int64_t> numels;
+  std::vector<uint32_t> group_begin;  // n + 1 chunk indices
+  DzChunk* d_chunks = nullptr;
+  uint32_t* d_group_begin = nullptr;
+  double* d_partials = nullptr;
+  DeviceState* dev = nullptr;
+};
+
+namespace {
+
+int32_t check_table(const dz_table* t) {
+  if (!t) return fail(DZ_ERR_INVALID, "table is NULL");
+  int dev;
+  int32_t rc = current_device(&dev);
+  if (rc) return rc;
+  if (dev != t->device) {
+    return fail(DZ_ERR_DEVICE, "table lives on device " + std::to_string(t->device) +
+                                   " but the current device is " + std::to_string(dev));
+  }
+  return DZ_OK;
+}
+
+void free_table(dz_table* t) {
+  if (t->d_chunks) (void)hipFree(t->d_chunks);
+  if (t->d_group_begin) (void)hipFree(t->d_group_begin);
+  if (t->d_partials) (void)hipFree(t->d_partials);
+  delete t;
+}
+
+// Optional per-group outputs must each hold t->n values.
+int32_t check_group_outputs(const dz_table* t, const double* d_sumsq, const float* d_norm_f32,
+                            const void* d_norm_T) {
+  int32_t rc = DZ_OK;
+  if (d_sumsq) rc = check_range((uint64_t)(uintptr_t)d_sumsq, (uint64_t)t->n * 8, "sumsq", 0);
+  if (!rc && d_norm_f32) rc = check_range((uint64_t)(uintptr_t)d_norm_f32, (uint64_t)t->n * 4, "norm_f32", 0);
+  if (!rc && d_norm_T)
+    rc = check_range((uint64_t)(uintptr_t)d_norm_T, (uint64_t)t->n * elem_size(t->dtype), "norm_T", 0);
+  return rc;
+}
+
+uint32_t rmw_grid(const dz_table* t) {
+  const uint32_t per_cu = (t->dtype == DZ_DTYPE_F32) ? 1u : 2u;  // LDS: 128 KB vs 64 KB table
+  const uint32_t g = per_cu * (uint32_t)t->dev->cus;
+  return t->nchunks < g ? t->nchunks : g;
+}
+
+int32_t rmw(dz_table* t, int mode, const dz::DzScalars& s, const dz::DzScalarPtrs& p, void* stream) {
+  int32_t rc = check_table(t);
+  if (rc) return rc;
+  if (t->projection) return fail(DZ_ERR_INVALID, "perturb/update need a ZO table (created without anchors)");
+  if (t->nchunks == 0) return DZ_OK;
+  hipError_t e = dz::launch_rmw(t->dtype, mode, t->d_chunks, t->nchunks, rmw_grid(t), t->dev->tab[t->dtype], s,
+                                p, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "rmw kernel launch");
+  return DZ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t dz_version(void) { return 100; }
+
+const char* dz_last_error(void) { return g_last_error.c_str(); }
+
+int32_t dz_normal_table(int32_t dtype, void* out, int64_t n_entries) {
+  if (!valid_dtype(dtype)) return fail(DZ_ERR_INVALID, "unknown dtype");
+  if (!out) return fail(DZ_ERR_INVALID, "out is NULL");
+  if (n_entries != kDzTabEntries) return fail(DZ_ERR_INVALID, "n_entries must be 32768");
+  memcpy(out, host_table_ptr(dtype), (size_t)kDzTabEntries * (size_t)elem_size(dtype));
+  return DZ_OK;
+}
+
+int32_t dz_philox_host(uint64_t seed, uint32_t stream_id, uint64_t q, uint32_t out[4]) {
+  if (!out) return fail(DZ_ERR_INVALID, "out is NULL");
+  const DzU4 w = dz_philox_group(seed, stream_id, q);
+  out[0] = w.x;
+  out[1] = w.y;
+  out[2] = w.z;
+  out[3] = w.w;
+  return DZ_OK;
+}
+
+int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const int64_t* numels,
+                        const uint64_t* z_offsets, int32_t n, int32_t dtype, int32_t device, dz_table** out) {
+  if (!out) return fail(DZ_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  if (!ptrs || !numels) return fail(DZ_ERR_INVALID, "ptrs/numels is NULL");
+  if (n <= 0 || n > (int32_t)kDzMetaGroupMask) return fail(DZ_ERR_INVALID, "tensor count out of range");
+  if (!valid_dtype(dtype)) return fail(DZ_ERR_INVALID, "unknown dtype");
+  int cur;
+  int32_t rc = current_device(&cur);
+  if (rc) return rc;
+  if (cur != device) {
+    return fail(DZ_ERR_DEVICE, "device " + std::to_string(device) + " is not the current device " +
+                                   std::to_string(cur));
+  }
+  DeviceState* ds = nullptr;
+  rc = ensure_device(device, &ds);
+  if (rc) return rc;
+
+  dz_table* t = new dz_table();
+  t->device = device;
+  t->dtype = dtype;
+  t->projection = anchor_ptrs != nullptr;
+  t->n = n;
+  t->dev = ds;
+  t->chunk_elems = t->projection ? (uint32_t)dz::kProjChunk : (uint32_t)dz::kRmwChunk;
+  const int es = elem_size(dtype);
+  std::vector<DzChunk> chunks;
+  uint64_t z = 0;
+  t->group_begin.push_back(0);
+  for (int32_t i = 0; i < n; ++i) {
+    const int64_t ne = numels[i];
+    if (ne < 0) {
+      free_table(t);
+      return fail(DZ_ERR_INVALID, "negative numel for tensor " + std::to_string(i));
+    }
+    const uint64_t p = ptrs[i];
+    const uint64_t a = t->projection ? anchor_ptrs[i] : 0;
+    if (z_offsets) {
+      if (z_offsets[i] % 8 != 0) {
+        free_table(t);
+        return fail(DZ_ERR_INVALID, "z offset of tensor " + std::to_string(i) + " is not a multiple of 8");
+      }
+      z = z_offsets[i];
+    }
+    if (ne > 0) {
+      rc = check_range(p, (uint64_t)ne * es, "theta", i);
+      if (!rc && t->projection) rc = check_range(a, (uint64_t)ne * es, "anchor", i);
+      if (rc) {
+        free_table(t);
+        return rc;
+      }
+    }
+    t->ptrs.push_back(p);
+    t->aux.push_back(a);
+    t->numels.push_back(ne);
+    t->zoff.push_back(z);
+    const bool aligned = (p % 16 == 0) && (a % 16 == 0);
+    for (int64_t s = 0; s < ne; s += t->chunk_elems) {
+      DzChunk c;
+      c.ptr = p + (uint64_t)s * es;
+      c.aux = t->projection ? a + (uint64_t)s * es : 0;
+      c.zgroup = (z + (uint64_t)s) >> 3;
+      c.n = (uint32_t)((ne - s) < (int64_t)t->chunk_elems ? (ne - s) : t->chunk_elems);
+      c.meta = (uint32_t)i | (aligned ? kDzMetaAligned : 0u);
+      chunks.push_back(c);
+      if (chunks.size() >= 0xffffffffull) {
+        free_table(t);
+        return fail(DZ_ERR_INVALID, "too many chunks");
+      }
+    }
+    t->group_begin.push_back((uint32_t)chunks.size());
+    z += ((uint64_t)ne + 7u) & ~(uint64_t)7u;
+  }
+  t->nchunks = (uint32_t)chunks.size();
+  hipError_t e = hipSuccess;
+  if (t->nchunks > 0) {
+    e = hipMalloc(&t->d_chunks, chunks.size() * sizeof(DzChunk));
+    if (e == hipSuccess)
+      e = hipMemcpy(t->d_chunks, chunks.data(), chunks.size() * sizeof(DzChunk), hipMemcpyHostToDevice);
+  }
+  if (e == hipSuccess && t->projection) {
+    // The finalize kernel always runs, so these exist even with no chunks.
+    e = hipMalloc(&t->d_group_begin, t->group_begin.size() * sizeof(uint32_t));
+    if (e == hipSuccess)
+      e = hipMemcpy(t->d_group_begin, t->group_begin.data(), t->group_begin.size() * sizeof(uint32_t),
+                    hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMalloc(&t->d_partials, (size_t)(t->nchunks ? t->nchunks : 1) * sizeof(double));
+  }
+  if (e != hipSuccess) {
+    free_table(t);
+    return hip_fail(e, "table upload");
+  }
+  *out = t;
+  return DZ_OK;
+}
+
+int32_t dz_table_destroy(dz_table* t) {
+  if (!t) return DZ_OK;
+  int cur = -1;
+  (void)hipGetDevice(&cur);
+  if (cur != t->device) (void)hipSetDevice(t->device);
+  // Kernels may still read the chunk list: wait for the device before freeing.
+  hipError_t e = hipDeviceSynchronize();
+  free_table(t);
+  if (cur >= 0 && cur != t->device) (void)hipSetDevice(cur);
+  if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize before table destroy");
+  return DZ_OK;
+}
+
+int32_t dz_table_matches(const dz_table* t, const uint64_t* ptrs, int32_t n) {
+  if (!t || !ptrs) return fail(DZ_ERR_INVALID, "NULL argument");
+  if (n != t->n) return 0;
+  for (int32_t i = 0; i < n; ++i)
+    if (ptrs[i] != t->ptrs[i]) return 0;
+  return 1;
+}
+
+int32_t dz_table_z_offset(const dz_table* t, int32_t idx, uint64_t* out) {
+  if (!t || !out) return fail(DZ_ERR_INVALID, "NULL argument");
+  if (idx < 0 || idx >= t->n) return fail(DZ_ERR_INVALID, "tensor index out of range");
+  *out = t->zoff[idx];
+  return DZ_OK;
+}
+
+int32_t dz_perturb(dz_table* t, uint64_t seed, float scale, float eps, const uint64_t* d_seed, void* stream) {
+  dz::DzScalars s{seed, scale, eps, 0.0f, 0.0f};
+  dz::DzScalarPtrs p{d_seed, nullptr, nullptr};
+  return rmw(t, dz::kModePerturb, s, p, stream);
+}
+
+int32_t dz_update(dz_table* t, uint64_t seed, float grad, float lr, const uint64_t* d_seed, const void* d_grad,
+                  const float* d_lr, void* stream) {
+  dz::DzScalars s{seed, 0.0f, 0.0f, grad, lr};
+  dz::DzScalarPtrs p{d_seed, d_grad, d_lr};
+  return rmw(t, dz::kModeUpdate, s, p, stream);
+}
+
+int32_t dz_restore_update(dz_table* t, uint64_t seed, float eps, float grad, float lr, const uint64_t* d_seed,
+                          const void* d_grad, const float* d_lr, void* stream) {
+  dz::DzScalars s{seed, 1.0f, eps, grad, lr};
+  dz::DzScalarPtrs p{d_seed, d_grad, d_lr};
+  return rmw(t, dz::kModeRestoreUpdate, s, p, stream);
+}
+
+int32_t dz_normals(uint64_t seed, uint32_t stream_id, uint64_t offset, int64_t n, int32_t dtype, void* d_out,
+                   void* stream) {
+  if (!valid_dtype(dtype)) return fail(DZ_ERR_INVALID, "unknown dtype");
+  // one thread per element, 256 per block: keep the grid below 2^31 blocks
+  if (n < 0 || n > ((int64_t)1 << 38)) return fail(DZ_ERR_INVALID, "n out of range");
+  if (n == 0) return DZ_OK;
+  int dev;
+  int32_t rc = current_device(&dev);
+  if (rc) return rc;
+  rc = check_range((uint64_t)(uintptr_t)d_out, (uint64_t)n * elem_size(dtype), "out", 0);
+  if (rc) return rc;
+  DeviceState* ds = nullptr;
+  rc = ensure_device(dev, &ds);
+  if (rc) return rc;
+  hipError_t e = dz::launch_normals(dtype, ds->tab[dtype], seed, stream_id, offset, (uint64_t)n, d_out,
+                                    (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "normals kernel launch");
+  return DZ_OK;
+}
+
+int32_t dz_export_z(const dz_table* t, uint64_t seed, int32_t idx, void* d_out, void* stream) {
+  int32_t rc = check_table(t);
+  if (rc) return rc;
+  if (t->projection) return fail(DZ_ERR_INVALID, "export needs a ZO table");
+  if (idx < 0 || idx >= t->n) return fail(DZ_ERR_INVALID, "tensor index out of range");
+  return dz_normals(seed, DZ_STREAM_PARAM, t->zoff[idx], t->numels[idx], t->dtype, d_out, stream);
+}
+
+int32_t dz_philox(uint64_t seed, uint32_t stream_id, uint64_t q0, int64_t n, uint32_t* d_out, void* stream) {
+  if (n < 0 || n > ((int64_t)1 << 36)) return fail(DZ_ERR_INVALID, "n out of range");
+  if (n == 0) return DZ_OK;
+  int32_t rc = check_range((uint64_t)(uintptr_t)d_out, (uint64_t)n * 16, "out", 0);
+  if (rc) return rc;
+  hipError_t e = dz::launch_philox(seed, stream_id, q0, (uint64_t)n, d_out, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "philox kernel launch");
+  return DZ_OK;
+}
+
+int32_t dz_group_sumsq(dz_table* t, double* d_sumsq, float* d_norm_f32, void* d_norm_T, void* stream) {
+  int32_t rc = check_table(t);
+  if (rc) return rc;
+  if (!t->projection) return fail(DZ_ERR_INVALID, "group_sumsq needs a projection table");
+  rc = check_group_outputs(t, d_sumsq, d_norm_f32, d_norm_T);
+  if (rc) return rc;
+  hipError_t e = hipSuccess;
+  if (t->nchunks > 0) {
+    e = dz::launch_proj(t->dtype, dz::kProjSumsq, t->d_chunks, t->nchunks, nullptr, t->d_partials,
+                        (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "sumsq kernel launch");
+  }
+  e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_sumsq, d_norm_f32,
+                          d_norm_T, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
+  return DZ_OK;
+}
+
+int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sumsq, float* d_norm_f32,
+                   void* d_norm_T, void* stream) {
+  int32_t rc = check_table(t);
+  if (rc) return rc;
+  if (!t->projection) return fail(DZ_ERR_INVALID, "project needs a projection table");
+  if (mode != DZ_PROJ_APPLY && mode != DZ_PROJ_REVERSE && mode != DZ_PROJ_REVERSE_SUMSQ)
+    return fail(DZ_ERR_INVALID, "mode must be APPLY, REVERSE or REVERSE_SUMSQ");
+  rc = check_range((uint64_t)(uintptr_t)d_alpha, (uint64_t)t->n * elem_size(t->dtype), "alpha", 0);
+  if (!rc) rc = check_group_outputs(t, d_sumsq, d_norm_f32, d_norm_T);
+  if (rc) return rc;
+  if (t->nchunks > 0) {
+    hipError_t e = dz::launch_proj(t->dtype, mode, t->d_chunks, t->nchunks, d_alpha, t->d_partials,
+                                   (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "projection kernel launch");
+  }
+  if (mode == DZ_PROJ_REVERSE_SUMSQ) {
+    hipError_t e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_sumsq,
+                                       d_norm_f32, d_norm_T, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
+  }
+  return DZ_OK;
+}
+
+}  // extern "C"

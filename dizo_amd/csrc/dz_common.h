@@ -1,0 +1,102 @@
+// Shared host/device definitions for the DiZO zeroth-order step kernels.
+//
+// Contents:
+//   * dtype codes used across the C ABI,
+//   * the chunk descriptor that the multi-tensor kernels walk,
+//   * Philox4x32-10, the counter-based generator that regenerates z in registers,
+//   * the z definition: z(seed, e) for global element index e.
+//
+// Philox4x32-10 follows Salmon, Moraes, Dror and Shaw, "Parallel Random Numbers:
+// As Easy as 1, 2, 3" (SC'11): four 32-bit counter words, a two-word key, ten
+// rounds of two 32x32->64 multiplies by 0xD2511F53 / 0xCD9E8D57, with the key
+// bumped by the Weyl constants 0x9E3779B9 / 0xBB67AE85 between rounds.
+//
+// z definition (replaces torch.normal at trainer.py:1441 and :1607):
+//   key  = (seed mod 2^32, seed >> 32)
+//   e    = global element index (tensors laid end to end, each tensor starting
+//          at a multiple of 8, in named_parameters_to_optim order)
+//   w    = Philox4x32-10(counter = (q mod 2^32, q >> 32, stream, 0), key), q = e >> 3
+//   h    = 16-bit field (e & 7) of w (field j = bits 16*(j&1).. of word j>>1)
+//   z    = (h & 0x8000 ? -1 : +1) * Q_T[h & 0x7fff]
+//   Q_T[i] = RNE_T( Phi^{-1}( 1/2 + (i + 1/2) / 65536 ) )
+// i.e. a sign bit and a 15-bit quantile index per element: eight normals per
+// Philox call, each already exact in the parameter dtype T.
+#pragma once
+#include <stdint.h>
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#include <hip/hip_runtime.h>
+#define DZ_HD __host__ __device__ __forceinline__
+#else
+#define DZ_HD static inline
+#endif
+
+enum DzDtype : int32_t { DZ_F32 = 0, DZ_F16 = 1, DZ_BF16 = 2 };
+
+// Stream ids of the Philox counter word 2.
+constexpr uint32_t kDzStreamParam = 0;  // z of the parameter perturbation / update
+constexpr uint32_t kDzStreamGamma = 1;  // z of the DiZO gamma perturbation (trainer.py:554)
+constexpr uint32_t kDzStreamInit = 2;   // synthetic weight initialisation
+
+constexpr int kDzTabEntries = 32768;  // quantile table entries (15-bit index)
+
+// One unit of work of a multi-tensor kernel: up to `chunk_elems` consecutive
+// elements of one tensor. Built on the host, uploaded once per table.
+struct DzChunk {
+  uint64_t ptr;     // byte address of the chunk's first element (theta)
+  uint64_t aux;     // byte address of the matching anchor element (theta0), or 0
+  uint64_t zgroup;  // Philox counter q of the chunk's first element (e / 8)
+  uint32_t n;       // number of elements in the chunk
+  uint32_t meta;    // bits 0..23: tensor/group index; bit 31: all pointers 16-byte aligned
+};
+static_assert(sizeof(DzChunk) == 32, "DzChunk must stay 32 bytes");
+
+constexpr uint32_t kDzMetaAligned = 0x80000000u;
+constexpr uint32_t kDzMetaGroupMask = 0x00ffffffu;
+
+struct DzU4 {
+  uint32_t x, y, z, w;
+};
+
+DZ_HD void dz_mulhilo32(uint32_t a, uint32_t b, uint32_t* lo, uint32_t* hi) {
+  const uint64_t p = (uint64_t)a * (uint64_t)b;
+  *lo = (uint32_t)p;
+  *hi = (uint32_t)(p >> 32);
+}
+
+// Philox4x32 with R rounds (R = 10 is the variant used everywhere here).
+template <int R>
+DZ_HD DzU4 dz_philox4x32(DzU4 c, uint32_t k0, uint32_t k1) {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+#endif
+  for (int r = 0; r < R; ++r) {
+    uint32_t lo0, hi0, lo1, hi1;
+    dz_mulhilo32(0xD2511F53u, c.x, &lo0, &hi0);
+    dz_mulhilo32(0xCD9E8D57u, c.z, &lo1, &hi1);
+    DzU4 n;
+    n.x = hi1 ^ c.y ^ k0;
+    n.y = lo1;
+    n.z = hi0 ^ c.w ^ k1;
+    n.w = lo0;
+    c = n;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c;
+}
+
+DZ_HD DzU4 dz_philox_group(uint64_t seed, uint32_t stream, uint64_t q) {
+  DzU4 c;
+  c.x = (uint32_t)q;
+  c.y = (uint32_t)(q >> 32);
+  c.z = stream;
+  c.w = 0u;
+  return dz_philox4x32<10>(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+}
+
+// 16-bit field j (0..7) of a Philox output block.
+DZ_HD uint32_t dz_field16(const DzU4& w, int j) {
+  const uint32_t word = (j >> 1) == 0 ? w.x : (j >> 1) == 1 ? w.y : (j >> 1) == 2 ? w.z : w.w;
+  return (word >> (16 * (j & 1))) & 0xffffu;
+}

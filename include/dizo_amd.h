@@ -1,0 +1,140 @@
+/*
+ * dizo_amd.h -- C ABI of the MI355X (gfx950) DiZO zeroth-order step kernels.
+ *
+ * Plain C: no torch or C++ types cross this boundary. Tensors are owned by
+ * the caller (PyTorch); the library only stores their device addresses. All
+ * functions return DZ_OK (0) or a negative DZ_ERR_* code; dz_last_error()
+ * returns the calling thread's last message. Work is enqueued asynchronously
+ * on the `stream` argument (a hipStream_t, NULL = legacy default stream);
+ * nothing synchronises except dz_table_create/destroy. The caller keeps every
+ * registered storage alive and in place while a table refers to it.
+ *
+ * References below are file:line in luozoupi/DiZO, large_models/trainer.py.
+ */
+#ifndef DIZO_AMD_H
+#define DIZO_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DZ_DTYPE_F32 0
+#define DZ_DTYPE_F16 1
+#define DZ_DTYPE_BF16 2
+
+#define DZ_OK 0
+#define DZ_ERR_INVALID (-1) /* bad argument (null, size, dtype, range)      */
+#define DZ_ERR_HIP (-2)     /* a HIP runtime call failed                    */
+#define DZ_ERR_DEVICE (-3)  /* current device differs from the table's one   */
+#define DZ_ERR_RANGE (-4)   /* pointer range outside its device allocation  */
+
+#define DZ_PROJ_SUMSQ 0         /* partial sums only (norm of theta - theta0)  */
+#define DZ_PROJ_APPLY 1         /* theta <- theta0 + (theta - theta0) * alpha  */
+#define DZ_PROJ_REVERSE 2       /* theta <- theta0 + (theta - theta0) / alpha  */
+#define DZ_PROJ_REVERSE_SUMSQ 3 /* REVERSE, then the norms of the new theta    */
+
+#define DZ_STREAM_PARAM 0u /* z of parameter perturbation / update */
+#define DZ_STREAM_GAMMA 1u /* z of the DiZO gamma perturbation     */
+#define DZ_STREAM_INIT 2u  /* synthetic weight initialisation      */
+
+typedef struct dz_table dz_table;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int32_t dz_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* dz_last_error(void);
+
+/* ---- host-only helpers (no GPU needed) --------------------------------- */
+
+/* Copies the 32768-entry quantile table Q_T (bit patterns of T) that maps a
+ * 15-bit index to |z|: Q_T[i] = RNE_T(Phi^-1(1/2 + (i + 1/2)/65536)).
+ * `out` holds n_entries elements of 2 (f16/bf16) or 4 (f32) bytes.
+ * Replaces the normal transform inside torch.normal, trainer.py:1441,1607. */
+int32_t dz_normal_table(int32_t dtype, void* out, int64_t n_entries);
+
+/* Philox4x32-10 block for key = seed, counter = (q, stream, 0), on the host. */
+int32_t dz_philox_host(uint64_t seed, uint32_t stream_id, uint64_t q, uint32_t out[4]);
+
+/* ---- parameter tables --------------------------------------------------- */
+
+/* Registers n tensors of one dtype on `device`. ptrs[i] is the device address
+ * of tensor i (numels[i] elements, contiguous). With anchor_ptrs == NULL the
+ * table is a ZO table (perturb/update); with anchor_ptrs the table is a
+ * projection table whose tensor i is group i with anchor theta0_i.
+ * z_offsets (may be NULL) gives each tensor's global z index (a multiple of
+ * 8); NULL lays the tensors end to end from 0, each rounded up to 8 elements.
+ * Each address range is checked against its device allocation.
+ * Replaces the trainable-set walk of trainer.py:1147-1160 (ZO table) and the
+ * exclude_list walk of trainer.py:405-451, 581-584 (projection table). */
+int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const int64_t* numels,
+                        const uint64_t* z_offsets, int32_t n, int32_t dtype, int32_t device,
+                        dz_table** out);
+int32_t dz_table_destroy(dz_table* t);
+
+/* 1 if the table was built from exactly these n addresses, else 0 (<0 on error). */
+int32_t dz_table_matches(const dz_table* t, const uint64_t* ptrs, int32_t n);
+
+/* Global z offset (element index of the tensor's first element) of tensor idx. */
+int32_t dz_table_z_offset(const dz_table* t, int32_t idx, uint64_t* out);
+
+/* ---- ZO step (trainer.py:1429-1444, 1570-1617) -------------------------- */
+/* Optional device pointers (NULL = use the by-value argument):
+ *   d_seed: uint64 seed;  d_grad: projected_grad as one element of the table
+ *   dtype;  d_lr: fp32 learning rate. They let a captured graph replay with
+ *   new values. */
+
+/* theta <- R(theta + R(R(scale*z)*eps)) for every registered tensor.
+ * Replaces zo_perturb_parameters(random_seed, scaling_factor), trainer.py:1429-1444. */
+int32_t dz_perturb(dz_table* t, uint64_t seed, float scale, float eps, const uint64_t* d_seed,
+                   void* stream);
+
+/* theta <- R(theta - R(lr*R(grad*z))).
+ * Replaces the parameter loop of zo_update, trainer.py:1603-1608. */
+int32_t dz_update(dz_table* t, uint64_t seed, float grad, float lr, const uint64_t* d_seed,
+                  const void* d_grad, const float* d_lr, void* stream);
+
+/* The restore of zo_step (scaling_factor = +1, trainer.py:1593) followed by
+ * the update of zo_update (trainer.py:1603-1608), in one pass: z is
+ * regenerated once and every element is read and written once. */
+int32_t dz_restore_update(dz_table* t, uint64_t seed, float eps, float grad, float lr,
+                          const uint64_t* d_seed, const void* d_grad, const float* d_lr,
+                          void* stream);
+
+/* ---- z export / RNG (test and tooling use) ------------------------------ */
+
+/* n normals z(seed, stream_id, offset + i) in `dtype`, written densely to d_out.
+ * The materialised z of trainer.py:1441 (random_vector, :1444). */
+int32_t dz_normals(uint64_t seed, uint32_t stream_id, uint64_t offset, int64_t n, int32_t dtype,
+                   void* d_out, void* stream);
+
+/* The z that dz_perturb/dz_update apply to tensor idx of a ZO table. */
+int32_t dz_export_z(const dz_table* t, uint64_t seed, int32_t idx, void* d_out, void* stream);
+
+/* n Philox blocks (4 x uint32 each) for counters q0 .. q0+n-1. */
+int32_t dz_philox(uint64_t seed, uint32_t stream_id, uint64_t q0, int64_t n, uint32_t* d_out,
+                  void* stream);
+
+/* ---- DiZO projection (trainer.py:405-465, 564-614) ----------------------- */
+
+/* Per group g: d_sumsq[g] = sum fp32(R(theta-theta0))^2 (fp64 accumulation),
+ * d_norm_f32[g] = sqrt_f32(fp32(sumsq)), d_norm_T[g] = R_T(norm): the
+ * torch.norm(theta - theta0) of trainer.py:455-457 and :583. Any output may be NULL. */
+int32_t dz_group_sumsq(dz_table* t, double* d_sumsq, float* d_norm_f32, void* d_norm_T,
+                       void* stream);
+
+/* mode DZ_PROJ_APPLY / DZ_PROJ_REVERSE / DZ_PROJ_REVERSE_SUMSQ with one alpha
+ * per group (device array of the table dtype). APPLY replaces the copy_ of
+ * apply_constraints (trainer.py:428-436); REVERSE replaces reverse_constraints
+ * (trainer.py:447-451); REVERSE_SUMSQ also writes the norms of the reversed
+ * theta (the next _project_ratio, trainer.py:455-457) to the outputs. */
+int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sumsq,
+                   float* d_norm_f32, void* d_norm_T, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DIZO_AMD_H */

@@ -1,0 +1,120 @@
+"""The reference's hot-path expressions written with torch ops (test oracle only).
+
+Each function evaluates the same torch expression the reference evaluates,
+in the same operand order, but takes z (and, for DiZO, the gamma noise and
+the losses) as inputs instead of drawing them from torch's generator. Run on
+CPU it pins ``oracle.arith`` against torch's real CPU kernels; run on the
+ROCm device (GPU box) it pins the HIP kernels against torch's device kernels,
+which is what the reference executes. On CPU it is also the timed CPU
+baseline of the reference's step (``bench.py``).
+"""
+from __future__ import annotations
+
+from typing import Callable, Sequence
+
+import torch
+
+
+def zo_perturb_parameters(params: Sequence[torch.Tensor], zs: Sequence[torch.Tensor],
+                          scaling_factor: float, zo_eps: float) -> None:
+    """trainer.py:1438-1442 with z supplied: param.data = param.data + s * z * eps."""
+    for param, z in zip(params, zs):
+        param.data = param.data + scaling_factor * z * zo_eps
+
+
+def zo_update(params: Sequence[torch.Tensor], zs: Sequence[torch.Tensor], projected_grad: float,
+              lr: float) -> None:
+    """trainer.py:1603-1608 with z supplied: param.data = param.data - lr * (g * z)."""
+    for param, z in zip(params, zs):
+        param.data = param.data - lr * (projected_grad * z)
+
+
+def zo_perturb_parameters_sampled(params: Sequence[torch.Tensor], seed: int, scaling_factor: float,
+                                  zo_eps: float) -> None:
+    """trainer.py:1438-1442 verbatim, z drawn by torch.normal (the CPU-baseline workload)."""
+    torch.manual_seed(seed)
+    for param in params:
+        z = torch.normal(mean=0, std=1, size=param.data.size(), device=param.data.device,
+                         dtype=param.data.dtype)
+        param.data = param.data + scaling_factor * z * zo_eps
+
+
+def zo_update_sampled(params: Sequence[torch.Tensor], seed: int, projected_grad: float, lr: float) -> None:
+    """trainer.py:1603-1608 verbatim (torch.normal z)."""
+    torch.manual_seed(seed)
+    for param in params:
+        z = torch.normal(mean=0, std=1, size=param.data.size(), device=param.data.device,
+                         dtype=param.data.dtype)
+        param.data = param.data - lr * (projected_grad * z)
+
+
+def projected_grad(loss1: torch.Tensor, loss2: torch.Tensor, zo_eps: float) -> float:
+    """trainer.py:1587."""
+    return ((loss1 - loss2) / (2 * zo_eps)).item()
+
+
+def project_ratio(new: torch.Tensor, anchor: torch.Tensor, constraint: torch.Tensor) -> torch.Tensor:
+    """trainer.py:453-465 (l2norm mode)."""
+    t = new.detach() - anchor.detach()
+    norms = torch.norm(t)
+    return constraint / (norms + 1e-8)
+
+
+def apply_constraints(news: Sequence[torch.Tensor], anchors: Sequence[torch.Tensor],
+                      constraints: Sequence[torch.Tensor]) -> list:
+    """trainer.py:405-436 over the projected tensors; returns the alphas."""
+    alphas = []
+    for new_para, anchor_para, c in zip(news, anchors, constraints):
+        alpha = project_ratio(new_para, anchor_para, c)
+        alphas.append(alpha)
+        v = (new_para.detach() - anchor_para.detach()) * alpha
+        temp = v + anchor_para.detach()
+        with torch.no_grad():
+            new_para.copy_(temp)
+    return alphas
+
+
+def reverse_constraints(news: Sequence[torch.Tensor], anchors: Sequence[torch.Tensor],
+                        alphas: Sequence[torch.Tensor]) -> None:
+    """trainer.py:439-451."""
+    for new_para, anchor_para, alpha in zip(news, anchors, alphas):
+        v = (new_para.detach() - anchor_para.detach()) / alpha
+        temp = v + anchor_para.detach()
+        with torch.no_grad():
+            new_para.copy_(temp)
+
+
+def dizo_zo_iteration(news, anchors, gammas: list, init: bool, z_gamma: Sequence[torch.Tensor],
+                      loss_fn: Callable[[int], torch.Tensor]):
+    """One ZO gamma iteration, trainer.py:564-614, with the gamma noise and the
+    two losses supplied (loss_fn(k) is the k-th forward's loss, k = 0, 1).
+
+    gammas: list of per-group gamma tensors (updated in place of the list).
+    Returns (ts, loss1, loss2).
+    """
+    with torch.no_grad():
+        ts = [torch.norm(p.data - a.data) for p, a in zip(news, anchors)]
+        if init:
+            for i in range(len(gammas)):
+                gammas[i] = ts[i]
+        tau, zo_eps, step_size = 0.2, 0.1, 2
+        zs = []
+        for i in range(len(gammas)):  # perturb_gamma(1, ...), trainer.py:553-560
+            z = torch.clip(z_gamma[i], (-tau / zo_eps) * ts[i], (tau / zo_eps) * ts[i])
+            zs.append(z)
+            gammas[i] = gammas[i] + 1 * z * zo_eps
+        alphas = apply_constraints(news, anchors, gammas)
+        loss1 = loss_fn(0)
+        reverse_constraints(news, anchors, alphas)
+        for i in range(len(gammas)):
+            gammas[i] = gammas[i] + -2 * zs[i] * zo_eps
+        alphas = apply_constraints(news, anchors, gammas)
+        loss2 = loss_fn(1)
+        reverse_constraints(news, anchors, alphas)
+        for i in range(len(gammas)):
+            gammas[i] = gammas[i] + 1 * zs[i] * zo_eps
+        grad = (loss1 - loss2) / (2 * zo_eps)
+        for i in range(len(gammas)):
+            gammas[i] = torch.clip(gammas[i] - step_size * ts[i] * grad * zs[i], (1 - tau) * ts[i],
+                                   (1 + tau) * ts[i])
+    return ts, loss1, loss2

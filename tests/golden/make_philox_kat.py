@@ -1,0 +1,83 @@
+"""Writes tests/golden/philox_kat.json: Philox4x32-10 known answers.
+
+Two independent sources:
+  * the Random123 known-answer vectors for philox4x32-10 (Salmon et al.,
+    SC'11 distribution, kat_vectors), typed in below;
+  * PyTorch's header-only engine ``at::Philox4_32`` (ATen/core/PhiloxRNGEngine.h,
+    BSD source shipped with the installed torch), compiled with g++ and run
+    for a set of (seed, subsequence, offset) triples. That engine keys
+    Philox with the seed and uses counter = (offset, subsequence), so its
+    first output block equals our block for key = seed,
+    counter = (q = offset, stream = subsequence).
+
+Run: python tests/golden/make_philox_kat.py
+"""
+from __future__ import annotations
+
+import json
+import os
+import subprocess
+import tempfile
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+RANDOM123_KAT = [
+    # counter (4 x u32), key (2 x u32), expected output (4 x u32)
+    [[0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]],
+    [[0xFFFFFFFF] * 4, [0xFFFFFFFF, 0xFFFFFFFF], [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]],
+    [[0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0],
+     [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]],
+]
+
+CASES = [  # (seed, subsequence = stream, offset = q)
+    (0, 0, 0), (1, 0, 0), (26, 0, 1), (123456789, 0, 7), (999999999, 1, 12345),
+    (2**32 + 3, 2, 2**32 + 11), (2**64 - 1, 0, 2**64 - 1), (42, 1, 2**40), (7, 0, 3_000_000_000),
+]
+
+PROG = r"""
+#include <ATen/core/PhiloxRNGEngine.h>
+#include <cstdio>
+#include <cstdlib>
+int main(int argc, char** argv) {
+  for (int i = 1; i + 2 < argc; i += 3) {
+    unsigned long long seed = strtoull(argv[i], 0, 10), sub = strtoull(argv[i+1], 0, 10),
+                       off = strtoull(argv[i+2], 0, 10);
+    at::Philox4_32 eng(seed, sub, off);
+    unsigned a = eng(), b = eng(), c = eng(), d = eng();
+    printf("%u %u %u %u\n", a, b, c, d);
+  }
+  return 0;
+}
+"""
+
+
+def torch_engine_blocks(cases):
+    inc = os.path.join(os.path.dirname(torch.__file__), "include")
+    with tempfile.TemporaryDirectory() as td:
+        src = os.path.join(td, "kat.cpp")
+        exe = os.path.join(td, "kat")
+        with open(src, "w") as f:
+            f.write(PROG)
+        subprocess.run(["g++", "-O1", "-std=c++17", f"-I{inc}", src, "-o", exe], check=True)
+        args = [str(x) for c in cases for x in c]
+        out = subprocess.run([exe, *args], check=True, capture_output=True, text=True).stdout
+    return [[int(x) for x in line.split()] for line in out.strip().splitlines()]
+
+
+def main():
+    blocks = torch_engine_blocks(CASES)
+    data = {
+        "random123": RANDOM123_KAT,
+        "torch_engine": [{"seed": s, "stream": sub, "q": off, "block": b}
+                         for (s, sub, off), b in zip(CASES, blocks)],
+        "source": "tests/golden/make_philox_kat.py",
+    }
+    with open(os.path.join(HERE, "philox_kat.json"), "w") as f:
+        json.dump(data, f, indent=1)
+    print(f"wrote {len(blocks)} torch-engine blocks")
+
+
+if __name__ == "__main__":
+    main()

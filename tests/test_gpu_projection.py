@@ -1,0 +1,123 @@
+"""GPU parity of the DiZO projection kernels (group norms, apply, reverse)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import arith as A
+from oracle import ref_torch as R
+from oracle.arith import BF16, F16, F32, from_f32, to_f32
+
+from tests._util import DT_TORCH, assert_bits_equal, random_theta, to_bits, to_torch
+
+pytestmark = pytest.mark.gpu
+
+DTS = [F16, BF16, F32]
+SIZES = [8192, 8191, 8193, 5, 64 * 64 * 5 + 3, 300000]
+
+
+def _groups(dt, seed, sizes=SIZES, rel=1e-2):
+    dev = torch.device("cuda", 0)
+    r = np.random.default_rng(seed)
+    th_h, t0_h = [], []
+    for i, n in enumerate(sizes):
+        t0 = random_theta(n, dt, seed + i, with_edges=False)
+        th = from_f32(to_f32(t0, dt) + (r.standard_normal(n) * 0.02 * rel).astype(np.float32), dt)
+        th_h.append(th)
+        t0_h.append(t0)
+    ths = [to_torch(x, dt, dev) for x in th_h]
+    t0s = [to_torch(x, dt, dev) for x in t0_h]
+    return ths, t0s, th_h, t0_h
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_group_norms(dt):
+    from dizo_amd.table import ProjTable
+    ths, t0s, th_h, t0_h = _groups(dt, 1)
+    tab = ProjTable(ths, t0s)
+    G = len(ths)
+    dev = ths[0].device
+    sumsq = torch.empty(G, dtype=torch.float64, device=dev)
+    nf = torch.empty(G, dtype=torch.float32, device=dev)
+    nt = torch.empty(G, dtype=DT_TORCH[dt], device=dev)
+    tab.group_sumsq(sumsq, nf, nt)
+    for g in range(G):
+        want = A.group_sumsq(th_h[g], t0_h[g], dt)
+        assert float(sumsq[g]) == pytest.approx(want, rel=1e-12)
+        n_or = A.norm_from_sumsq(want, dt)
+        assert abs(int(to_bits(nt[g:g + 1])[0]) - int(n_or)) <= 1
+        # and within one ulp of torch.norm on the device (what the reference computes)
+        tn = to_bits(torch.norm(ths[g] - t0s[g]).reshape(1))[0]
+        assert abs(int(to_bits(nt[g:g + 1])[0]) - int(tn)) <= 1
+    tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_apply_reverse_match_oracle(dt):
+    from dizo_amd._lib import DZ_PROJ_APPLY, DZ_PROJ_REVERSE, DZ_PROJ_REVERSE_SUMSQ
+    from dizo_amd.table import ProjTable
+    ths, t0s, th_h, t0_h = _groups(dt, 5)
+    tab = ProjTable(ths, t0s)
+    G = len(ths)
+    dev = ths[0].device
+    alphas = from_f32(np.linspace(0.85, 1.1, G).astype(np.float32), dt)
+    alpha_t = to_torch(alphas, dt, dev)
+    tab.project(alpha_t, DZ_PROJ_APPLY)
+    app = [A.apply(th_h[g], t0_h[g], alphas[g:g + 1], dt) for g in range(G)]
+    for g in range(G):
+        assert_bits_equal(to_bits(ths[g]), app[g], dt, f"apply group {g}")
+    sumsq = torch.empty(G, dtype=torch.float64, device=dev)
+    nt = torch.empty(G, dtype=DT_TORCH[dt], device=dev)
+    tab.project(alpha_t, DZ_PROJ_REVERSE_SUMSQ, sumsq=sumsq, norm_T=nt)
+    rev = [A.reverse(app[g], t0_h[g], alphas[g:g + 1], dt) for g in range(G)]
+    for g in range(G):
+        assert_bits_equal(to_bits(ths[g]), rev[g], dt, f"reverse group {g}")
+        want = A.group_sumsq(rev[g], t0_h[g], dt)
+        assert float(sumsq[g]) == pytest.approx(want, rel=1e-12)
+    # the fused norms equal a standalone norm pass over the same theta
+    s2 = torch.empty(G, dtype=torch.float64, device=dev)
+    tab.group_sumsq(s2)
+    assert torch.equal(sumsq, s2)
+    tab.project(alpha_t, DZ_PROJ_REVERSE)
+    rev2 = [A.reverse(rev[g], t0_h[g], alphas[g:g + 1], dt) for g in range(G)]
+    for g in range(G):
+        assert_bits_equal(to_bits(ths[g]), rev2[g], dt, f"reverse2 group {g}")
+    tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_apply_reverse_match_torch_on_device(dt):
+    """apply_constraints / reverse_constraints of the reference run by ROCm torch."""
+    from dizo_amd._lib import DZ_PROJ_APPLY, DZ_PROJ_REVERSE
+    from dizo_amd.table import ProjTable
+    ths, t0s, th_h, t0_h = _groups(dt, 9, sizes=[8192, 4099, 70000])
+    ref = [t.clone() for t in ths]
+    G = len(ths)
+    gammas = [0.9 * torch.norm(ths[g] - t0s[g]) for g in range(G)]
+    alphas = R.apply_constraints(ref, t0s, gammas)
+    alpha_t = torch.stack([a.reshape(()) for a in alphas]).contiguous()
+    tab = ProjTable(ths, t0s)
+    tab.project(alpha_t, DZ_PROJ_APPLY)
+    for g in range(G):
+        assert_bits_equal(to_bits(ths[g]), to_bits(ref[g]), dt, f"apply group {g}")
+    R.reverse_constraints(ref, t0s, alphas)
+    tab.project(alpha_t, DZ_PROJ_REVERSE)
+    for g in range(G):
+        assert_bits_equal(to_bits(ths[g]), to_bits(ref[g]), dt, f"reverse group {g}")
+    tab.close()
+
+
+def test_empty_and_rejects():
+    from dizo_amd._lib import DZ_PROJ_APPLY, DzError
+    from dizo_amd.table import ProjTable
+    dev = torch.device("cuda", 0)
+    a = [torch.zeros(0, device=dev), torch.ones(10, device=dev)]
+    b = [torch.zeros(0, device=dev), torch.zeros(10, device=dev)]
+    tab = ProjTable(a, b)
+    s = torch.empty(2, dtype=torch.float64, device=dev)
+    tab.group_sumsq(s)
+    assert s.tolist() == [0.0, 10.0]
+    with pytest.raises(DzError):
+        tab.project(torch.ones(3, device=dev), DZ_PROJ_APPLY)  # wrong alpha length
+    with pytest.raises(DzError):
+        ProjTable(a, [torch.zeros(0, device=dev), torch.zeros(11, device=dev)])
+    tab.close()

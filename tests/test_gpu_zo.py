@@ -1,0 +1,203 @@
+"""GPU parity of the ZO step kernels (perturb / update / restore+update / z export).
+
+Compared bit for bit against
+  * the numpy oracle (oracle.arith + oracle.rng computes z itself), and
+  * torch on the ROCm device evaluating the reference's expressions
+    (oracle.ref_torch) fed the z exported by the library.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import arith as A
+from oracle import ref_torch as R
+from oracle import rng
+from oracle.arith import BF16, F16, F32
+
+from tests._util import DT_TORCH, assert_bits_equal, random_theta, to_bits, to_torch
+
+pytestmark = pytest.mark.gpu
+
+DTS = [F16, BF16, F32]
+# sizes: tiny, odd, group-aligned, one chunk (32768), chunk + 1, several chunks
+SIZES = [1, 7, 8, 9, 1000, 32768, 32769, 3 * 50000, 65536 + 24, 2050 * 64, 0, 5]
+
+
+def _make_tensors(dt, seed, sizes=SIZES, misaligned=(3, 6)):
+    """Device tensors with oracle-generated contents; some are views whose data
+    pointer is not 16-byte aligned."""
+    dev = torch.device("cuda", 0)
+    tensors, host = [], []
+    keep = []
+    for i, n in enumerate(sizes):
+        bits = random_theta(n, dt, seed + i) if n else np.zeros(0, A.BITS_DTYPE[dt])
+        t = to_torch(bits, dt, dev)
+        if i in misaligned and n:
+            buf = torch.empty(n + 1, dtype=t.dtype, device=dev)
+            view = buf[1:]
+            view.copy_(t)
+            keep.append(buf)
+            t = view
+        tensors.append(t)
+        host.append(bits)
+    return tensors, host, keep
+
+
+def _z_host(table, seed, dt):
+    return [rng.tensor_z_bits(seed, off, n, dt) for off, n in zip(table.z_offsets, table.numels)]
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_z_export_matches_oracle(dt):
+    from dizo_amd.table import ZOTable, normals
+    tensors, _, keep = _make_tensors(dt, 100)
+    tab = ZOTable(tensors)
+    seed = 987654321
+    for i, t in enumerate(tensors):
+        z = tab.export_z(seed, i)
+        assert_bits_equal(to_bits(z).ravel(), rng.tensor_z_bits(seed, tab.z_offsets[i], t.numel(), dt), dt,
+                          f"export z tensor {i}")
+    # dense normals at an unaligned offset and in the gamma stream
+    for stream, off in ((0, 13), (1, 0), (2, 2**33 + 5)):
+        z = normals(seed, stream, off, 5000, DT_TORCH[dt], torch.device("cuda", 0))
+        assert_bits_equal(to_bits(z), rng.z_bits(seed, stream, np.arange(5000, dtype=np.uint64) + np.uint64(off), dt),
+                          dt, f"normals stream {stream}")
+    tab.close()
+
+
+def test_philox_blocks_match_oracle():
+    from dizo_amd.table import philox_blocks
+    for seed, stream, q0 in ((0, 0, 0), (26, 1, 2**32 - 3), (2**64 - 1, 2, 2**40)):
+        got = philox_blocks(seed, stream, q0, 4096, torch.device("cuda", 0)).cpu().numpy().view(np.uint32)
+        want = rng.philox_groups(seed, stream, np.arange(4096, dtype=np.uint64) + np.uint64(q0))
+        np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_rmw_uses_exported_z(dt):
+    """theta = 0, scale 1, eps 1 leaves exactly z: the kernel's in-register z is the exported z."""
+    from dizo_amd.table import ZOTable
+    dev = torch.device("cuda", 0)
+    tensors = [torch.zeros(n, dtype=DT_TORCH[dt], device=dev) for n in (5, 40000, 32768 * 3 + 7)]
+    tab = ZOTable(tensors)
+    tab.perturb(31337, 1.0, 1.0)
+    for i, t in enumerate(tensors):
+        assert_bits_equal(to_bits(t), to_bits(tab.export_z(31337, i)).ravel(), dt, f"tensor {i}")
+    tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("scale", [1.0, -2.0, 0.5])
+def test_perturb_matches_oracle(dt, scale):
+    from dizo_amd.table import ZOTable
+    tensors, host, keep = _make_tensors(dt, 7)
+    tab = ZOTable(tensors)
+    seed, eps = 123456789, 1e-3
+    tab.perturb(seed, scale, eps)
+    for i, (t, h, z) in enumerate(zip(tensors, host, _z_host(tab, seed, dt))):
+        assert_bits_equal(to_bits(t).ravel(), A.perturb(h, z, scale, eps, dt), dt, f"tensor {i} n={h.size}")
+    tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_full_step_sequence_matches_oracle(dt):
+    """perturb +1, -2, then fused restore+update; and the unfused restore, update."""
+    from dizo_amd.table import ZOTable
+    tensors, host, keep = _make_tensors(dt, 21)
+    tab = ZOTable(tensors)
+    seed, eps, g, lr = 424242, 1e-3, -0.734375, 9.93875e-07
+    zs = _z_host(tab, seed, dt)
+    tab.perturb(seed, 1.0, eps)
+    tab.perturb(seed, -2.0, eps)
+    want = [A.perturb(A.perturb(h, z, 1, eps, dt), z, -2, eps, dt) for h, z in zip(host, zs)]
+    for i, (t, w) in enumerate(zip(tensors, want)):
+        assert_bits_equal(to_bits(t).ravel(), w, dt, f"after -2, tensor {i}")
+    clones = [t.clone() for t in tensors]
+    tab.restore_update(seed, eps, g, lr)
+    final = [A.restore_update(w, z, eps, g, lr, dt) for w, z in zip(want, zs)]
+    for i, (t, w) in enumerate(zip(tensors, final)):
+        assert_bits_equal(to_bits(t).ravel(), w, dt, f"fused, tensor {i}")
+    # the unfused path on the clones gives the same bits
+    for t, c in zip(tensors, clones):
+        t.copy_(c)
+    tab.perturb(seed, 1.0, eps)
+    tab.update(seed, g, lr)
+    for i, (t, w) in enumerate(zip(tensors, final)):
+        assert_bits_equal(to_bits(t).ravel(), w, dt, f"unfused, tensor {i}")
+    tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_device_scalar_overrides(dt):
+    """Seed / grad / lr read from device memory give the by-value results."""
+    from dizo_amd.table import ZOTable
+    tensors, host, keep = _make_tensors(dt, 33, sizes=[40000, 77])
+    tab = ZOTable(tensors)
+    seed, eps, g, lr = 55555, 1e-3, 1.25, 2e-6
+    dev = torch.device("cuda", 0)
+    d_seed = torch.tensor([seed], dtype=torch.int64, device=dev)
+    d_grad = torch.tensor(g, dtype=DT_TORCH[dt], device=dev)
+    d_lr = torch.tensor(lr, dtype=torch.float32, device=dev)
+    tab.perturb(0, 1.0, eps, d_seed=d_seed)
+    tab.restore_update(1, eps, 0.0, 0.0, d_seed=d_seed, d_grad=d_grad, d_lr=d_lr)
+    zs = _z_host(tab, seed, dt)
+    for i, (t, h, z) in enumerate(zip(tensors, host, zs)):
+        want = A.restore_update(A.perturb(h, z, 1, eps, dt), z, eps, g, lr, dt)
+        assert_bits_equal(to_bits(t).ravel(), want, dt, f"tensor {i}")
+    tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_matches_torch_on_device(dt):
+    """The reference's own expressions evaluated by ROCm torch, fed the exported z."""
+    from dizo_amd.table import ZOTable
+    tensors, host, keep = _make_tensors(dt, 40, sizes=[1, 9, 32769, 100000], misaligned=())
+    ref = [t.clone() for t in tensors]
+    tab = ZOTable(tensors)
+    seed, eps, g, lr = 777, 1e-3, 3.5, 1e-6
+    zs = [tab.export_z(seed, i) for i in range(len(tensors))]
+    for s in (1, -2, 1):
+        tab.perturb(seed, float(s), eps)
+        R.zo_perturb_parameters(ref, zs, s, eps)
+        for i, (t, r) in enumerate(zip(tensors, ref)):
+            assert_bits_equal(to_bits(t), to_bits(r), dt, f"s={s} tensor {i}")
+    tab.update(seed, g, lr)
+    R.zo_update(ref, zs, g, lr)
+    for i, (t, r) in enumerate(zip(tensors, ref)):
+        assert_bits_equal(to_bits(t), to_bits(r), dt, f"update tensor {i}")
+    tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_projected_grad_device_rule(dt):
+    """torch on the device divides by a python scalar via the fp32 reciprocal (the oracle's rule)."""
+    r = np.random.default_rng(2)
+    l1 = A.from_f32((r.random(512) * 3).astype(np.float32), dt)
+    l2 = A.from_f32((r.random(512) * 3).astype(np.float32), dt)
+    dev = torch.device("cuda", 0)
+    got = to_bits((to_torch(l1, dt, dev) - to_torch(l2, dt, dev)) / (2 * 1e-3))
+    d = A.from_f32(A.to_f32(l1, dt) - A.to_f32(l2, dt), dt)
+    assert_bits_equal(got, A.scalar_div_device(d, 2e-3, dt), dt, "device scalar div")
+
+
+def test_stale_table_raises():
+    from dizo_amd._lib import DzError
+    from dizo_amd.table import ZOTable
+    p = torch.nn.Parameter(torch.zeros(100, device="cuda"))
+    tab = ZOTable([p.data])
+    p.data = torch.ones(100, device="cuda")  # rebinding, as trainer.py:1442 does
+    tab.tensors[0] = p.data
+    with pytest.raises(DzError):
+        tab.check()
+    tab.close()
+
+
+def test_rejects_bad_inputs():
+    from dizo_amd._lib import DzError
+    from dizo_amd.table import ZOTable
+    with pytest.raises(DzError):
+        ZOTable([torch.zeros(4)])  # CPU tensor
+    with pytest.raises(DzError):
+        ZOTable([torch.zeros(4, device="cuda"), torch.zeros(4, device="cuda", dtype=torch.float16)])
+    with pytest.raises(DzError):
+        ZOTable([torch.zeros(4, 4, device="cuda").t()])  # non-contiguous
