@@ -191,6 +191,7 @@ struct dz_table {
   DzChunk* d_chunks = nullptr;
   uint32_t* d_group_begin = nullptr;
   double* d_partials = nullptr;
+  uint32_t* d_counters = nullptr;  // RMW work counters (ZO tables)
   DeviceState* dev = nullptr;
 };
 
@@ -212,6 +213,7 @@ void free_table(dz_table* t) {
   if (t->d_chunks) (void)hipFree(t->d_chunks);
   if (t->d_group_begin) (void)hipFree(t->d_group_begin);
   if (t->d_partials) (void)hipFree(t->d_partials);
+  if (t->d_counters) (void)hipFree(t->d_counters);
   delete t;
 }
 
@@ -226,8 +228,11 @@ int32_t check_group_outputs(const dz_table* t, const double* d_sumsq, const floa
   return rc;
 }
 
-uint32_t rmw_grid(const dz_table* t) {
-  const uint32_t per_cu = (t->dtype == DZ_DTYPE_F32) ? 1u : 2u;  // LDS: 128 KB vs 64 KB table
+// Persistent grid of an RMW launch: as many 1024-thread workgroups as fit on
+// the device at once given the LDS delta table (64 KB: two per CU; 128 KB:
+// one per CU), but no more than there are tiles.
+uint32_t rmw_grid(const dz_table* t, int mode) {
+  const uint32_t per_cu = dz::rmw_lds_table_bytes(t->dtype, mode) <= 65536 ? 2u : 1u;
   const uint32_t g = per_cu * (uint32_t)t->dev->cus;
   return t->nchunks < g ? t->nchunks : g;
 }
@@ -237,8 +242,8 @@ int32_t rmw(dz_table* t, int mode, const dz::DzScalars& s, const dz::DzScalarPtr
   if (rc) return rc;
   if (t->projection) return fail(DZ_ERR_INVALID, "perturb/update need a ZO table (created without anchors)");
   if (t->nchunks == 0) return DZ_OK;
-  hipError_t e = dz::launch_rmw(t->dtype, mode, t->d_chunks, t->nchunks, rmw_grid(t), t->dev->tab[t->dtype], s,
-                                p, (hipStream_t)stream);
+  hipError_t e = dz::launch_rmw(t->dtype, mode, t->d_chunks, t->nchunks, rmw_grid(t, mode), t->dev->tab[t->dtype],
+                                s, p, t->d_counters, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "rmw kernel launch");
   return DZ_OK;
 }
@@ -293,7 +298,7 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
   t->projection = anchor_ptrs != nullptr;
   t->n = n;
   t->dev = ds;
-  t->chunk_elems = t->projection ? (uint32_t)dz::kProjChunk : (uint32_t)dz::kRmwChunk;
+  t->chunk_elems = t->projection ? (uint32_t)dz::kProjChunk : (uint32_t)dz::rmw_chunk_elems(dtype);
   const int es = elem_size(dtype);
   std::vector<DzChunk> chunks;
   uint64_t z = 0;
@@ -356,6 +361,12 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
       e = hipMemcpy(t->d_group_begin, t->group_begin.data(), t->group_begin.size() * sizeof(uint32_t),
                     hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMalloc(&t->d_partials, (size_t)(t->nchunks ? t->nchunks : 1) * sizeof(double));
+  }
+  if (e == hipSuccess && !t->projection) {
+    // zeroed once here; every RMW launch leaves them at zero again
+    e = hipMalloc(&t->d_counters, dz::kCounterWords * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(t->d_counters, 0, dz::kCounterWords * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
   }
   if (e != hipSuccess) {
     free_table(t);

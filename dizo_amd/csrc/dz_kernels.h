@@ -7,18 +7,42 @@
 
 namespace dz {
 
-// Read-modify-write kernel geometry: 1024 threads x 4 groups x 8 elements.
+enum RmwMode : int { kModePerturb = 0, kModeUpdate = 1, kModeRestoreUpdate = 2 };
+enum ProjMode : int { kProjSumsq = 0, kProjApply = 1, kProjReverse = 2, kProjReverseSumsq = 3 };
+
+// Read-modify-write kernel geometry. A workgroup of 1024 threads takes one
+// tile (chunk) at a time from the table's work counters; each thread owns
+// kRmwGroups16 (16-bit T) or kRmwGroups32 (fp32) groups of 8 elements per
+// tile, i.e. 128 KB of theta per tile for every dtype.
 constexpr int kRmwThreads = 1024;
-constexpr int kUnroll = 4;
-constexpr int kRmwChunk = kRmwThreads * kUnroll * 8;  // 32768 elements
+constexpr int kRmwGroups16 = 8;
+constexpr int kRmwGroups32 = 4;
+constexpr int kRmwChunk16 = kRmwThreads * kRmwGroups16 * 8;  // 65536 elements
+constexpr int kRmwChunk32 = kRmwThreads * kRmwGroups32 * 8;  // 32768 elements
+__host__ __device__ constexpr int rmw_chunk_elems(int dtype) {
+  return dtype == DZ_F32 ? kRmwChunk32 : kRmwChunk16;
+}
+
+// LDS bytes of the per-launch delta table of an RMW launch: 16-bit entries
+// for perturb/update of 16-bit T, 32-bit entries otherwise (fp32 deltas, or
+// the (restore delta, update delta) pair of a fused restore+update).
+__host__ __device__ constexpr int rmw_lds_table_bytes(int dtype, int mode) {
+  return (dtype == DZ_F32 || mode == kModeRestoreUpdate) ? kDzTabEntries * 4 : kDzTabEntries * 2;
+}
+
+// Work counters of a table, one set per table: kCounters tile dispensers 128
+// bytes apart, then the number of finished workgroups. Zeroed when the table
+// is created; the last workgroup of every RMW launch puts them back to zero,
+// so consecutive launches on one stream need no reset (and no memset in a
+// captured graph). Launches of one table must not overlap in time.
+constexpr int kCounters = 8;
+constexpr int kCounterStride = 32;  // uint32 slots (128 bytes)
+constexpr int kCounterWords = (kCounters + 1) * kCounterStride;
 
 // Projection kernel geometry: 256 threads x 32 elements (16-bit T: 4 x 16 B,
 // fp32: 8 x 16 B per thread).
 constexpr int kProjThreads = 256;
 constexpr int kProjChunk = 8192;
-
-enum RmwMode : int { kModePerturb = 0, kModeUpdate = 1, kModeRestoreUpdate = 2 };
-enum ProjMode : int { kProjSumsq = 0, kProjApply = 1, kProjReverse = 2, kProjReverseSumsq = 3 };
 
 // By-value scalars of one RMW launch.
 struct DzScalars {
@@ -38,7 +62,8 @@ struct DzScalarPtrs {
 };
 
 hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
-                      const void* tab, const DzScalars& s, const DzScalarPtrs& p, hipStream_t st);
+                      const void* qtab, const DzScalars& s, const DzScalarPtrs& p, uint32_t* counters,
+                      hipStream_t st);
 hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, const void* alpha,
                        double* partials, hipStream_t st);
 hipError_t launch_finalize(int dtype, const double* partials, const uint32_t* gbegin, uint32_t ngroups,

@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "dz_common.h"
 #include "dz_kernels.h"
 
@@ -86,32 +88,6 @@ __device__ __forceinline__ uint32_t op_update(float th, float z, float g, float 
   return DT_<DT>::from_f(th - d);
 }
 
-template <int DT, int MODE>
-__device__ __forceinline__ uint32_t op_rmw(uint32_t thb, uint32_t zb, const DzScalars& s) {
-  const float th = DT_<DT>::to_f(thb);
-  const float z = DT_<DT>::to_f(zb);
-  if constexpr (MODE == kModePerturb) {
-    return op_perturb<DT>(th, z, s.scale, s.eps);
-  } else if constexpr (MODE == kModeUpdate) {
-    return op_update<DT>(th, z, s.grad, s.lr);
-  } else {  // kModeRestoreUpdate
-    // trainer.py:1593 (restore, scaling_factor=+1) then trainer.py:1608.
-    const float th1 = DT_<DT>::to_f(op_perturb<DT>(th, z, 1.0f, s.eps));
-    return op_update<DT>(th1, z, s.grad, s.lr);
-  }
-}
-
-// z bits of field j of a Philox block, from the LDS quantile table.
-template <int DT>
-__device__ __forceinline__ uint32_t z_bits(const typename DT_<DT>::S* tab, uint32_t h) {
-  const uint32_t mag = (uint32_t)tab[h & 0x7fffu];
-  return mag | ((h & 0x8000u) << (DT_<DT>::kBits - 16));
-}
-
-__device__ __forceinline__ uint32_t word_of(const DzU4& w, int i) {
-  return i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w;
-}
-
 template <int DT>
 __device__ __forceinline__ float load_scalar_T(const void* p) {
   return DT_<DT>::to_f((uint32_t)(*(const typename DT_<DT>::S*)p));
@@ -125,96 +101,255 @@ __device__ __forceinline__ DzScalars resolve_scalars(DzScalars s, const DzScalar
   return s;
 }
 
+__device__ __forceinline__ uint32_t word_of(const DzU4& w, int i) {
+  return i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w;
+}
+
+// z bits of a 16-bit field h (sign bit + 15-bit index) from a quantile table.
+template <int DT>
+__device__ __forceinline__ uint32_t z_bits(const typename DT_<DT>::S* tab, uint32_t h) {
+  const uint32_t mag = (uint32_t)tab[h & 0x7fffu];
+  return mag | ((h & 0x8000u) << (DT_<DT>::kBits - 16));
+}
+
 // ---------------------------------------------------------------------------
-// Multi-tensor read-modify-write kernel (perturb / update / restore+update).
-// Persistent workgroups walk the chunk list; each thread owns kUnroll groups
-// of 8 consecutive elements per chunk (one Philox call each). The 15-bit
-// quantile table lives in LDS.
+// Per-launch delta tables.
+//
+// Every z is +-Q_T[i] for a 15-bit index i, and each of the reference's
+// per-element expressions adds an odd function of z to theta:
+//   perturb  theta' = R(theta + b),     b = R(R(s*z)*eps)      trainer.py:1442
+//   update   theta' = R(theta - d),     d = R(lr*R(g*z))       trainer.py:1608
+//                   = R(theta + (-d))   (x - y is x + (-y) in IEEE arithmetic,
+//                                        signed zeros included)
+// RNE rounding is symmetric in sign, so b(-z) = -b(z) and d(-z) = -d(z). A
+// launch evaluates b, or -d, once per table index (32768 entries in LDS, with
+// exactly the arithmetic above), and each element then costs one lookup, a
+// sign flip and the final add. The fused restore+update keeps the pair
+// (b, -d) per entry for 16-bit T. For 16-bit T the final add is done in T:
+// fp16 adds natively; bf16 adds in fp32 and rounds to bf16 (the reference's
+// own recipe). fp32 carries 24 >= 2p+2 significand bits for p = 11, so the
+// fp16 sum rounded once equals the fp32 sum rounded to fp16.
+// fp32 tables hold the fp32 delta bits, or for restore+update z itself (the
+// pair would not fit in LDS) with b and d evaluated per element.
 // ---------------------------------------------------------------------------
 template <int DT, int MODE>
-__global__ void __launch_bounds__(kRmwThreads) rmw_kernel(const DzChunk* __restrict__ chunks,
-                                                          uint32_t nchunks,
-                                                          const void* __restrict__ gtab,
-                                                          DzScalars sc_in, DzScalarPtrs sp) {
-  using S = typename DT_<DT>::S;
-  __shared__ __attribute__((aligned(16))) S tab[kDzTabEntries];
-  {
-    const uint4* src = (const uint4*)gtab;
-    uint4* dst = (uint4*)tab;
-    constexpr int kVecs = (int)(kDzTabEntries * sizeof(S) / 16);
-    for (int i = threadIdx.x; i < kVecs; i += kRmwThreads) dst[i] = src[i];
-  }
-  const DzScalars sc = resolve_scalars<DT>(sc_in, sp);
-  __syncthreads();
+struct RmwTraits {
+  static constexpr bool kWide = (DT == DZ_F32 || MODE == kModeRestoreUpdate);
+  using E = typename std::conditional<kWide, uint32_t, uint16_t>::type;
+  static constexpr int kGroups = DT == DZ_F32 ? kRmwGroups32 : kRmwGroups16;
+  static constexpr int kChunk = kRmwThreads * kGroups * 8;
+  // Waves per SIMD when the LDS table lets two workgroups share a CU (the
+  // register budget then is 64 VGPRs), else one workgroup (4 waves).
+  static constexpr int kWavesPerEU = kWide ? 4 : 8;
+};
 
-  constexpr int kES = (int)sizeof(S);
-  for (uint32_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
-    const DzChunk ch = chunks[c];
-    const bool aligned = (ch.meta & kDzMetaAligned) != 0u;
-    char* base = (char*)ch.ptr;
-    if (ch.n == (uint32_t)kRmwChunk && aligned) {
-      if constexpr (kES == 2) {
-        uint4 v[kUnroll];
+// Table entry for z = +Q_T[i] (qbits = bits of Q_T[i]).
+template <int DT, int MODE>
+__device__ __forceinline__ uint32_t table_entry(uint32_t qbits, const DzScalars& sc) {
+  constexpr uint32_t kSign = DT == DZ_F32 ? 0x80000000u : 0x8000u;
+  const float z = DT_<DT>::to_f(qbits);
+  const float b = rt<DT>(rt<DT>(sc.scale * z) * sc.eps);
+  const float d = rt<DT>(sc.lr * rt<DT>(sc.grad * z));
+  if constexpr (MODE == kModePerturb) {
+    return DT_<DT>::from_f(b);
+  } else if constexpr (MODE == kModeUpdate) {
+    return DT_<DT>::from_f(d) ^ kSign;
+  } else if constexpr (DT == DZ_F32) {
+    return qbits;
+  } else {
+    return DT_<DT>::from_f(b) | ((DT_<DT>::from_f(d) ^ kSign) << 16);
+  }
+}
+
+typedef _Float16 dz_half2 __attribute__((ext_vector_type(2)));
+
+// R_T(a + b) for a pair of 16-bit values packed in one word.
+template <int DT>
+__device__ __forceinline__ uint32_t add_pair(uint32_t a, uint32_t b) {
+  if constexpr (DT == DZ_F16) {
+    const dz_half2 x = __builtin_bit_cast(dz_half2, a);
+    const dz_half2 y = __builtin_bit_cast(dz_half2, b);
+    return __builtin_bit_cast(uint32_t, x + y);
+  } else {
+    const float a0 = __uint_as_float(a << 16), a1 = __uint_as_float(a & 0xffff0000u);
+    const float b0 = __uint_as_float(b << 16), b1 = __uint_as_float(b & 0xffff0000u);
+    return DT_<DT>::from_f(a0 + b0) | (DT_<DT>::from_f(a1 + b1) << 16);
+  }
+}
+
+// R_T(a + b) for one 16-bit value.
+template <int DT>
+__device__ __forceinline__ uint32_t add_one(uint32_t a, uint32_t b) {
+  if constexpr (DT == DZ_F16) {
+    const _Float16 r = __builtin_bit_cast(_Float16, (uint16_t)a) + __builtin_bit_cast(_Float16, (uint16_t)b);
+    return (uint32_t)__builtin_bit_cast(uint16_t, r);
+  } else {
+    return DT_<DT>::from_f(__uint_as_float(a << 16) + __uint_as_float(b << 16));
+  }
+}
+
+// Two 16-bit elements (packed in `th`) whose z fields are the halves of `w`.
+template <int DT, int MODE>
+__device__ __forceinline__ uint32_t apply_pair16(uint32_t th, uint32_t w, const typename RmwTraits<DT, MODE>::E* tab) {
+  if constexpr (MODE != kModeRestoreUpdate) {
+    const uint32_t lo = (uint32_t)tab[w & 0x7fffu] ^ (w & 0x8000u);
+    const uint32_t hi = (uint32_t)tab[(w >> 16) & 0x7fffu] ^ ((w >> 16) & 0x8000u);
+    return add_pair<DT>(th, lo | (hi << 16));
+  } else {
+    // entry = b | (-d) << 16; a negative z negates both halves
+    const uint32_t e0 = tab[w & 0x7fffu] ^ ((w & 0x8000u) * 0x10001u);
+    const uint32_t e1 = tab[(w >> 16) & 0x7fffu] ^ (((w >> 16) & 0x8000u) * 0x10001u);
+    const uint32_t b = (e0 & 0xffffu) | (e1 << 16);
+    const uint32_t nd = (e0 >> 16) | (e1 & 0xffff0000u);
+    return add_pair<DT>(add_pair<DT>(th, b), nd);
+  }
+}
+
+// One element with 16-bit z field h.
+template <int DT, int MODE>
+__device__ __forceinline__ uint32_t apply_one(uint32_t th, uint32_t h, const typename RmwTraits<DT, MODE>::E* tab,
+                                              const DzScalars& sc) {
+  if constexpr (DT == DZ_F32) {
+    const uint32_t e = tab[h & 0x7fffu] ^ ((h & 0x8000u) << 16);
+    if constexpr (MODE != kModeRestoreUpdate) {
+      return __float_as_uint(__uint_as_float(th) + __uint_as_float(e));
+    } else {
+      const float z = __uint_as_float(e);
+      const float th1 = __uint_as_float(op_perturb<DZ_F32>(__uint_as_float(th), z, 1.0f, sc.eps));
+      return op_update<DZ_F32>(th1, z, sc.grad, sc.lr);
+    }
+  } else if constexpr (MODE != kModeRestoreUpdate) {
+    return add_one<DT>(th, (uint32_t)tab[h & 0x7fffu] ^ (h & 0x8000u));
+  } else {
+    const uint32_t e = tab[h & 0x7fffu] ^ ((h & 0x8000u) * 0x10001u);
+    return add_one<DT>(add_one<DT>(th, e & 0xffffu), e >> 16);
+  }
+}
+
+typedef uint32_t dz_u32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming 16-byte accesses: theta is touched once per pass, so loads and
+// stores carry the non-temporal hint.
+__device__ __forceinline__ dz_u32x4 ld_stream(const void* p) {
+  return __builtin_nontemporal_load((const dz_u32x4*)p);
+}
+__device__ __forceinline__ void st_stream(void* p, dz_u32x4 v) {
+  __builtin_nontemporal_store(v, (dz_u32x4*)p);
+}
+
+// One tile of an RMW launch.
+template <int DT, int MODE>
+__device__ __forceinline__ void rmw_chunk(const DzChunk& ch, const typename RmwTraits<DT, MODE>::E* tab,
+                                          const DzScalars& sc) {
+  using Tr = RmwTraits<DT, MODE>;
+  using S = typename DT_<DT>::S;
+  constexpr int G = Tr::kGroups;
+  char* base = (char*)ch.ptr;
+  if (ch.n == (uint32_t)Tr::kChunk && (ch.meta & kDzMetaAligned) != 0u) {
+    if constexpr (DT != DZ_F32) {
+      dz_u32x4 v[G];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const uint32_t g = threadIdx.x + u * kRmwThreads;
-          v[u] = *(const uint4*)(base + (size_t)g * 16);
-        }
+      for (int u = 0; u < G; ++u) v[u] = ld_stream(base + (size_t)(threadIdx.x + u * kRmwThreads) * 16);
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const uint32_t g = threadIdx.x + u * kRmwThreads;
-          const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
-          uint32_t in[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-          uint32_t out[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t wi = word_of(w, i);
-            const uint32_t z0 = z_bits<DT>(tab, wi & 0xffffu);
-            const uint32_t z1 = z_bits<DT>(tab, wi >> 16);
-            const uint32_t r0 = op_rmw<DT, MODE>(in[i] & 0xffffu, z0, sc);
-            const uint32_t r1 = op_rmw<DT, MODE>(in[i] >> 16, z1, sc);
-            out[i] = (r0 & 0xffffu) | (r1 << 16);
-          }
-          *(uint4*)(base + (size_t)g * 16) = make_uint4(out[0], out[1], out[2], out[3]);
-        }
-      } else {
-        uint4 v[kUnroll][2];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const uint32_t g = threadIdx.x + u * kRmwThreads;
-          v[u][0] = *(const uint4*)(base + (size_t)g * 32);
-          v[u][1] = *(const uint4*)(base + (size_t)g * 32 + 16);
-        }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const uint32_t g = threadIdx.x + u * kRmwThreads;
-          const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
-          uint32_t in[8] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w,
-                            v[u][1].x, v[u][1].y, v[u][1].z, v[u][1].w};
-          uint32_t out[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const uint32_t h = (word_of(w, j >> 1) >> (16 * (j & 1))) & 0xffffu;
-            out[j] = op_rmw<DT, MODE>(in[j], z_bits<DT>(tab, h), sc);
-          }
-          *(uint4*)(base + (size_t)g * 32) = make_uint4(out[0], out[1], out[2], out[3]);
-          *(uint4*)(base + (size_t)g * 32 + 16) = make_uint4(out[4], out[5], out[6], out[7]);
-        }
+      for (int u = 0; u < G; ++u) {
+        const uint32_t g = threadIdx.x + u * kRmwThreads;
+        const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
+        dz_u32x4 o;
+        o.x = apply_pair16<DT, MODE>(v[u].x, w.x, tab);
+        o.y = apply_pair16<DT, MODE>(v[u].y, w.y, tab);
+        o.z = apply_pair16<DT, MODE>(v[u].z, w.z, tab);
+        o.w = apply_pair16<DT, MODE>(v[u].w, w.w, tab);
+        st_stream(base + (size_t)g * 16, o);
       }
     } else {
-      // Partial or misaligned chunk: per-group, per-element with bounds checks.
-      for (int u = 0; u < kUnroll; ++u) {
-        const uint32_t g = threadIdx.x + u * kRmwThreads;
-        const uint32_t e0 = g * 8u;
-        if (e0 >= ch.n) continue;
-        const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
-        const uint32_t m = min(8u, ch.n - e0);
-        for (uint32_t j = 0; j < m; ++j) {
-          const uint32_t h = (word_of(w, (int)(j >> 1)) >> (16 * (j & 1))) & 0xffffu;
-          S* p = (S*)(base + (size_t)(e0 + j) * kES);
-          *p = (S)op_rmw<DT, MODE>((uint32_t)*p, z_bits<DT>(tab, h), sc);
-        }
+      dz_u32x4 v[G][2];
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        const size_t off = (size_t)(threadIdx.x + u * kRmwThreads) * 32;
+        v[u][0] = ld_stream(base + off);
+        v[u][1] = ld_stream(base + off + 16);
       }
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        const uint32_t g = threadIdx.x + u * kRmwThreads;
+        const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
+        dz_u32x4 o0, o1;
+        o0.x = apply_one<DT, MODE>(v[u][0].x, w.x & 0xffffu, tab, sc);
+        o0.y = apply_one<DT, MODE>(v[u][0].y, w.x >> 16, tab, sc);
+        o0.z = apply_one<DT, MODE>(v[u][0].z, w.y & 0xffffu, tab, sc);
+        o0.w = apply_one<DT, MODE>(v[u][0].w, w.y >> 16, tab, sc);
+        o1.x = apply_one<DT, MODE>(v[u][1].x, w.z & 0xffffu, tab, sc);
+        o1.y = apply_one<DT, MODE>(v[u][1].y, w.z >> 16, tab, sc);
+        o1.z = apply_one<DT, MODE>(v[u][1].z, w.w & 0xffffu, tab, sc);
+        o1.w = apply_one<DT, MODE>(v[u][1].w, w.w >> 16, tab, sc);
+        st_stream(base + (size_t)g * 32, o0);
+        st_stream(base + (size_t)g * 32 + 16, o1);
+      }
+    }
+  } else {
+    // Partial or misaligned tile: element by element, bounds-checked.
+    for (uint32_t g = threadIdx.x; g * 8u < ch.n; g += kRmwThreads) {
+      const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
+      const uint32_t m = min(8u, ch.n - g * 8u);
+      for (uint32_t j = 0; j < m; ++j) {
+        const uint32_t h = (word_of(w, (int)(j >> 1)) >> (16 * (j & 1))) & 0xffffu;
+        S* p = (S*)(base + (size_t)(g * 8u + j) * sizeof(S));
+        *p = (S)apply_one<DT, MODE>((uint32_t)*p, h, tab, sc);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Multi-tensor read-modify-write kernel (perturb / update / restore+update).
+// Persistent workgroups build the launch's delta table in LDS, then take
+// tiles from the table's work counters (counter j of the K in use hands out
+// tiles j, j + K, j + 2K, ...; workgroup b uses counter (b / 8) mod K, so each
+// counter serves workgroups on every XCD, and K = min(8, grid / 8) so each
+// counter has workgroups). Handing out tiles dynamically keeps the tiles in
+// flight close together in memory and lets fast workgroups take more tiles,
+// which a static grid-stride split does not; the next tile index is fetched
+// while the current tile is processed. The last workgroup to finish resets
+// the counters for the next launch.
+// ---------------------------------------------------------------------------
+template <int DT, int MODE>
+__global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU)) rmw_kernel(const DzChunk* __restrict__ chunks,
+                                                          uint32_t nchunks,
+                                                          const void* __restrict__ qtab,
+                                                          DzScalars sc_in, DzScalarPtrs sp,
+                                                          uint32_t* __restrict__ counters) {
+  using Tr = RmwTraits<DT, MODE>;
+  using E = typename Tr::E;
+  using S = typename DT_<DT>::S;
+  __shared__ __attribute__((aligned(16))) E tab[kDzTabEntries];
+  __shared__ uint32_t slot[2];
+  const DzScalars sc = resolve_scalars<DT>(sc_in, sp);
+  {
+    const S* q = (const S*)qtab;
+    for (int i = threadIdx.x; i < kDzTabEntries; i += kRmwThreads)
+      tab[i] = (E)table_entry<DT, MODE>((uint32_t)q[i], sc);
+  }
+  // Counters in use: every one of them must be served by at least one
+  // workgroup, or its tiles would never be taken (a small grid uses fewer).
+  const uint32_t ncnt = max(1u, min((uint32_t)kCounters, gridDim.x >> 3));
+  const uint32_t j = (blockIdx.x >> 3) % ncnt;
+  uint32_t* mine = counters + j * kCounterStride;
+  if (threadIdx.x == 0) slot[0] = atomicAdd(mine, 1u);
+  __syncthreads();
+  uint32_t k = 0;
+  uint64_t c = (uint64_t)slot[0] * ncnt + j;
+  while (c < nchunks) {
+    if (threadIdx.x == 0) slot[(k + 1) & 1] = atomicAdd(mine, 1u);
+    const uint32_t cu = __builtin_amdgcn_readfirstlane((uint32_t)c);
+    rmw_chunk<DT, MODE>(chunks[cu], tab, sc);
+    __syncthreads();
+    ++k;
+    c = (uint64_t)slot[k & 1] * ncnt + j;
+  }
+  if (threadIdx.x == 0) {
+    const uint32_t done = atomicAdd(counters + kCounters * kCounterStride, 1u);
+    if (done == gridDim.x - 1) {
+      for (int i = 0; i <= kCounters; ++i) atomicExch(counters + i * kCounterStride, 0u);
     }
   }
 }
@@ -386,19 +521,19 @@ __global__ void __launch_bounds__(256) philox_kernel(uint64_t seed, uint32_t str
 template <int DT>
 static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
                                 const void* tab, const DzScalars& s, const DzScalarPtrs& p,
-                                hipStream_t st) {
+                                uint32_t* counters, hipStream_t st) {
   switch (mode) {
     case kModePerturb:
       hipLaunchKernelGGL((rmw_kernel<DT, kModePerturb>), dim3(grid), dim3(kRmwThreads), 0, st,
-                         chunks, nchunks, tab, s, p);
+                         chunks, nchunks, tab, s, p, counters);
       break;
     case kModeUpdate:
       hipLaunchKernelGGL((rmw_kernel<DT, kModeUpdate>), dim3(grid), dim3(kRmwThreads), 0, st,
-                         chunks, nchunks, tab, s, p);
+                         chunks, nchunks, tab, s, p, counters);
       break;
     case kModeRestoreUpdate:
       hipLaunchKernelGGL((rmw_kernel<DT, kModeRestoreUpdate>), dim3(grid), dim3(kRmwThreads), 0,
-                         st, chunks, nchunks, tab, s, p);
+                         st, chunks, nchunks, tab, s, p, counters);
       break;
     default:
       return hipErrorInvalidValue;
@@ -407,11 +542,12 @@ static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunk
 }
 
 hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
-                      const void* tab, const DzScalars& s, const DzScalarPtrs& p, hipStream_t st) {
+                      const void* tab, const DzScalars& s, const DzScalarPtrs& p, uint32_t* counters,
+                      hipStream_t st) {
   switch (dtype) {
-    case DZ_F32: return launch_rmw_dt<DZ_F32>(mode, chunks, nchunks, grid, tab, s, p, st);
-    case DZ_F16: return launch_rmw_dt<DZ_F16>(mode, chunks, nchunks, grid, tab, s, p, st);
-    case DZ_BF16: return launch_rmw_dt<DZ_BF16>(mode, chunks, nchunks, grid, tab, s, p, st);
+    case DZ_F32: return launch_rmw_dt<DZ_F32>(mode, chunks, nchunks, grid, tab, s, p, counters, st);
+    case DZ_F16: return launch_rmw_dt<DZ_F16>(mode, chunks, nchunks, grid, tab, s, p, counters, st);
+    case DZ_BF16: return launch_rmw_dt<DZ_BF16>(mode, chunks, nchunks, grid, tab, s, p, counters, st);
     default: return hipErrorInvalidValue;
   }
 }

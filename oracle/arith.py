@@ -79,12 +79,16 @@ def restore_update(theta_bits, z_bits, eps, grad, lr, dt: str) -> np.ndarray:
 
 
 def scalar_div_device(x_bits, divisor: float, dt: str):
-    """T tensor / python scalar on a GPU: x * (1.0f / float(divisor)), one rounding to T.
+    """T tensor / python scalar on the GPU (trainer.py:1587 and :607).
 
-    PyTorch's CUDA/ROCm true-divide kernel multiplies by the fp32 reciprocal of
-    a CPU-scalar divisor (BinaryDivTrueKernel); trainer.py:1587 and :607 run it.
+    torch's device true-divide by a CPU scalar multiplies by a reciprocal
+    instead of dividing; the reciprocal is formed from the double-precision
+    scalar and rounded once to fp32, then R_T(x * inv). Pinned on the ROCm
+    device by tests/test_gpu_zo.py::test_projected_grad_device_rule (for
+    divisor 0.002 the rule x * fp32(1/0.002f) = x * 499.99997 differs from
+    torch in about 1% of fp16 inputs; this one matches bit for bit).
     """
-    inv = np.float32(1.0) / np.float32(divisor)
+    inv = np.float32(1.0 / float(divisor))
     return from_f32(to_f32(x_bits, dt) * inv, dt)
 
 

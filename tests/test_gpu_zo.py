@@ -168,16 +168,61 @@ def test_matches_torch_on_device(dt):
     tab.close()
 
 
+def _opt_like_sizes(target_elems: int, d: int = 768):
+    """Tensor sizes in OPT layer order (matrices, biases, layer norms) up to target_elems."""
+    out, total = [2050 * d], 2050 * d
+    while total < target_elems:
+        layer = [d * d, d] * 4 + [d, d, 4 * d * d, 4 * d, 4 * d * d, d, d, d]
+        out += layer
+        total += sum(layer)
+    return out + [d, d]
+
+
 @pytest.mark.parametrize("dt", DTS)
-def test_projected_grad_device_rule(dt):
-    """torch on the device divides by a python scalar via the fp32 reciprocal (the oracle's rule)."""
-    r = np.random.default_rng(2)
-    l1 = A.from_f32((r.random(512) * 3).astype(np.float32), dt)
-    l2 = A.from_f32((r.random(512) * 3).astype(np.float32), dt)
+@pytest.mark.parametrize("target", [200_000, 1_200_000, 6_000_000, 90_000_000])
+def test_multi_tile_launches_match_torch(dt, target):
+    """Tables of 3 to ~1400 tiles (grids below and above the counter fan-out,
+    several tiles per workgroup): every element is processed exactly once per
+    launch, also on consecutive launches (the work counters reset themselves).
+    Checked against the reference's expressions run by ROCm torch with the
+    exported z."""
+    from dizo_amd.table import ZOTable
     dev = torch.device("cuda", 0)
-    got = to_bits((to_torch(l1, dt, dev) - to_torch(l2, dt, dev)) / (2 * 1e-3))
+    sizes = _opt_like_sizes(target, d=64 if target < 1_000_000 else 768)
+    print(f"dt={dt} target={target} tensors={len(sizes)} elems={sum(sizes)}", flush=True)
+    gen = torch.Generator(device=dev).manual_seed(target)
+    tensors = [(torch.randn(n, device=dev, generator=gen) * 0.02).to(DT_TORCH[dt]) for n in sizes]
+    ref = [t.clone() for t in tensors]
+    tab = ZOTable(tensors)
+    seed, eps, g, lr = 1000 + target % 977, 1e-3, -2.25, 1e-6
+    zs = [tab.export_z(seed, i) for i in range(len(tensors))]
+    for s_ in (1, -2):
+        tab.perturb(seed, float(s_), eps)
+        R.zo_perturb_parameters(ref, zs, s_, eps)
+    tab.restore_update(seed, eps, g, lr)
+    R.zo_perturb_parameters(ref, zs, 1, eps)
+    R.zo_update(ref, zs, g, lr)
+    tab.update(seed, g, lr)
+    R.zo_update(ref, zs, g, lr)
+    torch.cuda.synchronize()
+    bad = [i for i, (t, r) in enumerate(zip(tensors, ref)) if not torch.equal(t.view(torch.int16 if dt != F32 else torch.int32),
+                                                                           r.view(torch.int16 if dt != F32 else torch.int32))]
+    assert not bad, f"{len(bad)} tensors differ, first {bad[:5]}"
+    tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("divisor", [2 * 1e-3, 2 * 0.1, 0.003, 0.7, 3.0])
+def test_projected_grad_device_rule(dt, divisor):
+    """torch on the device divides a T tensor by a python scalar as the oracle's
+    device rule says: R_T(x * fp32(1 / divisor)) with the reciprocal taken in double."""
+    r = np.random.default_rng(2)
+    l1 = A.from_f32((r.random(4096) * 3).astype(np.float32), dt)
+    l2 = A.from_f32((r.random(4096) * 3).astype(np.float32), dt)
+    dev = torch.device("cuda", 0)
+    got = to_bits((to_torch(l1, dt, dev) - to_torch(l2, dt, dev)) / divisor)
     d = A.from_f32(A.to_f32(l1, dt) - A.to_f32(l2, dt), dt)
-    assert_bits_equal(got, A.scalar_div_device(d, 2e-3, dt), dt, "device scalar div")
+    assert_bits_equal(got, A.scalar_div_device(d, divisor, dt), dt, f"device scalar div by {divisor}")
 
 
 def test_stale_table_raises():

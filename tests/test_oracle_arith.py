@@ -110,9 +110,9 @@ def test_bf16_rounding_matches_torch():
 
 @pytest.mark.parametrize("dt", DTS)
 def test_projected_grad_and_scalar_div(dt):
-    # CPU torch divides truly; the device rule multiplies by the fp32 reciprocal.
-    # Check the oracle's device rule against its definition and the CPU rule's
-    # closeness (at most one unit in the last place apart).
+    # CPU torch divides truly; the device rule multiplies by the reciprocal of
+    # the double scalar rounded to fp32. Check the device rule against its
+    # definition and its closeness to the CPU rule (at most one ulp apart).
     r = np.random.default_rng(1)
     l1 = from_f32((r.random(2000) * 2).astype(np.float32), dt)
     l2 = from_f32((r.random(2000) * 2).astype(np.float32), dt)
@@ -120,7 +120,7 @@ def test_projected_grad_and_scalar_div(dt):
     dev = A.scalar_div_device(d, 0.002, dt).astype(np.int64)
     cpu = to_bits(to_torch(d, dt) / 0.002).astype(np.int64)
     assert np.abs(dev - cpu).max() <= 1
-    want = to_f32(from_f32(to_f32(d, dt) * (np.float32(1) / np.float32(0.002)), dt), dt)
+    want = to_f32(from_f32(to_f32(d, dt) * np.float32(500.0), dt), dt)
     assert A.projected_grad(l1[:1], l2[:1], 1e-3, dt) == float(want[0])
     # the CPU rule is torch's CPU division, bit for bit
     assert_bits_equal(A.scalar_div_cpu(d, 0.002, dt), cpu.astype(np.uint64), dt, "cpu div")
