@@ -480,7 +480,8 @@ __global__ void __launch_bounds__(kProjThreads) finalize_kernel(const double* __
   for (uint32_t i = b + threadIdx.x; i < e; i += kProjThreads) x += partials[i];
   const double t = block_sum_f64(x, red);
   if (threadIdx.x == 0) {
-    const float n = sqrtf((float)t);
+    // correctly rounded fp32 sqrt of the fp32 sum (a double sqrt rounds once more, exactly)
+    const float n = (float)sqrt((double)(float)t);
     if (sumsq) sumsq[g] = t;
     if (norm_f32) norm_f32[g] = n;
     if (norm_T) ((S*)norm_T)[g] = (S)DT_<DT>::from_f(n);

@@ -1,0 +1,318 @@
+"""Drop-in DiZO layer-wise divergence projection on the HIP kernels.
+
+``DiZO`` and ``dizo_trainer`` keep the reference's names, constructor
+signatures, methods and state (luozoupi/DiZO, large_models/trainer.py):
+
+  DiZO(model, norm_mode, exclude_list)                        trainer.py:378-403
+    .apply_constraints(new, pre_trained, it, apply=False)     trainer.py:405-436
+    .reverse_constraints(new, pre_trained)                    trainer.py:439-451
+    ._project_ratio(new, anchor, it)                          trainer.py:453-465
+    .perturb_gamma(delta, ts, zs, tau, zo_eps)                trainer.py:545-562
+    .zo_forward(new, pre_trained, x, apply)                   trainer.py:564-614
+    state: constraints (ParameterList, one gamma per projected tensor),
+           alpha (dict), ts (list), init (bool)
+  dizo_trainer(base_model, pgmloader, norm_mode, proj_lr, max_iters, exclude_list)
+    .dizo_zo_iters(model, base_model, apply=False)            trainer.py:782-803
+    .dizo_iters(model, base_model, apply=False)               trainer.py:805-830
+
+The per-tensor loops of the reference become one launch over all projected
+tensors: a group sum-of-squares pass for the norms, and APPLY / REVERSE
+read-modify-write passes (REVERSE also returns the norms of the reversed
+tensors, which the next ratio needs). The per-group scalar arithmetic on
+gamma, the norms and alpha (clip, SPSA step, ratio) is evaluated elementwise
+over a (G,) tensor with the reference's expressions, which gives each group
+the reference's value.
+
+Differences from the reference, by design:
+  * gamma noise (torch.normal in perturb_gamma, trainer.py:554) comes from
+    the library's generator: stream DZ_STREAM_GAMMA keyed by the seed of the
+    ZO step that triggered the event, one draw of G normals per SPSA
+    iteration (``gamma_seed`` / draw counter);
+  * norms accumulate in fp64 and round once (torch.norm accumulates in fp32):
+    within one unit in the last place of the model dtype.
+"""
+from __future__ import annotations
+
+from typing import Dict, List, Optional, Sequence
+
+import torch
+from torch import nn
+
+from . import _lib as L
+from ._lib import DzError
+from .table import ProjTable, normals
+from .trainer import forward_wrap_with_option_len
+
+TAU, GAMMA_EPS, STEP_SIZE = 0.2, 0.1, 2  # trainer.py:590-592
+
+
+class DiZO(nn.Module):
+    """One gamma per projected tensor and the projection passes (trainer.py:378-614)."""
+
+    def __init__(self, model, norm_mode, exclude_list=[]) -> None:  # noqa: B006 (reference signature)
+        super().__init__()
+        if "l2" not in norm_mode:
+            # trainer.py:460: the per-row L1 ("MARS") branch is unreachable with the
+            # reference's only configuration, 'l2norm' (trainer.py:1168)
+            raise DzError(f"norm_mode {norm_mode!r}: only the l2 norm is implemented")
+        self.norm_mode = norm_mode
+        self.exclude_list = list(exclude_list)
+        self.threshold = nn.Hardtanh(0, 1)
+        self.constraints_name: List[str] = []
+        self.id_name_map: Dict[int, str] = {}
+        constraints = []
+        device = None
+        for name, para in model.named_parameters():
+            if name not in self.exclude_list and para.requires_grad:
+                self.constraints_name.append(name)
+                constraints.append(nn.Parameter(torch.Tensor([0]), requires_grad=True))
+                self.id_name_map[len(self.constraints_name) - 1] = name
+                if device is None and para.device.type == "cuda":
+                    device = para.device
+        if not constraints:
+            raise DzError("DiZO: no projected tensors (every parameter is excluded)")
+        self.constraints = nn.ParameterList(constraints)
+        self._device = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self._set_gamma(torch.zeros(len(constraints), dtype=torch.float32, device=self._device))
+        self.init = True
+        self.times = 0
+        self.alpha: Dict[str, torch.Tensor] = {}
+        self.n = {}
+        self.include_list: List[str] = []
+        self.ts: List[torch.Tensor] = []
+        # build state
+        self.gamma_seed = 0
+        self._draws = 0
+        self._tab: Optional[ProjTable] = None
+        self._tab_key = None
+        self._alpha_vec: Optional[torch.Tensor] = None
+        self._norms: Optional[torch.Tensor] = None  # norms of the current theta - theta0, when known
+        self._in_event = False  # the driver vouches that theta is unchanged since _norms
+        self.kernel_timer = None
+
+    # ---------------------------------------------------------- gamma ----
+    @property
+    def G(self) -> int:
+        return len(self.constraints_name)
+
+    def _set_gamma(self, vec: torch.Tensor) -> None:
+        """gamma lives in one (G,) tensor; each constraint Parameter views one element."""
+        vec = vec.reshape(-1).contiguous()
+        self._gamma = vec
+        for i, p in enumerate(self.constraints):
+            p.data = vec[i:i + 1]
+
+    def gamma(self) -> torch.Tensor:
+        """The (G,) gamma vector (constraint Parameters are views of it)."""
+        return self._gamma
+
+    # ---------------------------------------------------------- tables ---
+    def _table(self, new: nn.Module, pre_trained: nn.Module) -> ProjTable:
+        params = dict(new.named_parameters())
+        anchors = dict(pre_trained.named_parameters())
+        try:
+            th = [params[n].data for n in self.constraints_name]
+            t0 = [anchors[n].data for n in self.constraints_name]
+        except KeyError as e:
+            raise DzError(f"DiZO: parameter {e} missing from the model or its anchor") from None
+        key = (tuple(t.data_ptr() for t in th), tuple(t.data_ptr() for t in t0))
+        if self._tab is None or self._tab_key != key:
+            if self._tab is not None:
+                self._tab.close()
+            self._tab = ProjTable(th, t0)
+            self._tab_key = key
+            self._norms = None
+        return self._tab
+
+    def _timed(self, name: str, tab: ProjTable, passes: int, fn) -> None:
+        timer = self.kernel_timer
+        if timer is None:
+            fn()
+        else:
+            with timer.span(name, passes * tab.bytes_per_tensor_pass):
+                fn()
+
+    def _group_norms(self, tab: ProjTable) -> torch.Tensor:
+        """torch.norm(theta - theta0) of every group (trainer.py:455-457, 583), in T."""
+        norms = torch.empty(self.G, dtype=tab.dtype, device=tab.device)
+        self._timed("proj_sumsq", tab, 2, lambda: tab.group_sumsq(norm_T=norms))
+        return norms
+
+    def _ratio(self, norms: torch.Tensor) -> torch.Tensor:
+        """trainer.py:464  constraint / (norms + 1e-8), per group."""
+        return self._gamma / (norms + 1e-8)
+
+    def _apply_alpha(self, tab: ProjTable, alpha: torch.Tensor) -> None:
+        if alpha.dtype != tab.dtype:
+            raise DzError(f"DiZO: alpha is {alpha.dtype} but the projected tensors are {tab.dtype} "
+                          "(a float32 gamma is the first-order path, dizo_iters)")
+        alpha = alpha.contiguous()
+        self._timed("proj_apply", tab, 3, lambda: tab.project(alpha, L.DZ_PROJ_APPLY))
+        self._alpha_vec = alpha
+        self._norms = None
+        self.alpha = {name: alpha[i:i + 1] for i, name in enumerate(self.constraints_name)}
+        self.include_list = list(self.constraints_name)
+
+    def _reverse(self, tab: ProjTable) -> torch.Tensor:
+        """trainer.py:447-451 for every group, returning the norms of the reversed theta."""
+        if self._alpha_vec is None:
+            raise DzError("DiZO: reverse_constraints before apply_constraints")
+        norms = torch.empty(self.G, dtype=tab.dtype, device=tab.device)
+        self._timed("proj_reverse_sumsq", tab, 3,
+                    lambda: tab.project(self._alpha_vec, L.DZ_PROJ_REVERSE_SUMSQ, norm_T=norms))
+        self._norms = norms
+        return norms
+
+    @staticmethod
+    def _freeze(model: nn.Module) -> None:
+        for p in model.parameters():  # trainer.py:417, 444
+            p.requires_grad = False
+
+    # --------------------------------------------------- reference API ---
+    def apply_constraints(self, new, pre_trained, constraint_iterator, apply=False):
+        """trainer.py:405-436: theta <- theta0 + gamma / (||theta - theta0|| + 1e-8) * (theta - theta0)."""
+        tab = self._table(new, pre_trained)
+        gam = [next(constraint_iterator) for _ in range(self.G)]
+        if any(g.data.data_ptr() != self._gamma[i:i + 1].data_ptr() for i, g in enumerate(gam)):
+            self._set_gamma(torch.cat([g.data.reshape(1) for g in gam]))
+        trusted = self._in_event and self._norms is not None
+        norms = self._norms if trusted else self._group_norms(tab)
+        self._freeze(new)
+        self._apply_alpha(tab, self._ratio(norms))
+
+    def reverse_constraints(self, new, pre_trained):
+        """trainer.py:439-451: theta <- theta0 + (theta - theta0) / alpha."""
+        tab = self._table(new, pre_trained)
+        self._freeze(new)
+        self._reverse(tab)
+
+    def _project_ratio(self, new, anchor, constraint_iterator):
+        """trainer.py:453-465 for one projected tensor `new` with anchor `anchor`."""
+        if self._tab is None:
+            raise DzError("DiZO._project_ratio: no projection table yet (call apply_constraints first)")
+        ptrs = [t.data_ptr() for t in self._tab.tensors]
+        try:
+            i = ptrs.index(new.data_ptr())
+        except ValueError:
+            raise DzError("DiZO._project_ratio: tensor is not one of the projected tensors") from None
+        constraint = next(constraint_iterator)
+        norms = self._group_norms(self._tab)
+        return constraint / (norms[i] + 1e-8)
+
+    def _draw_gamma_z(self, dtype: torch.dtype) -> torch.Tensor:
+        """G standard normals for one perturb_gamma draw (trainer.py:554)."""
+        z = normals(self.gamma_seed, L.DZ_STREAM_GAMMA, self._draws * self.G, self.G, dtype, self._device)
+        self._draws += 1
+        return z
+
+    def perturb_gamma(self, delta, ts=None, zs=None, tau=None, zo_eps=None):
+        """trainer.py:545-562 over all groups: gamma <- gamma + delta * z * zo_eps,
+        z ~ N(0, 1) clipped to +-(tau / zo_eps) * ts (drawn when zs is None)."""
+        if zs is None:
+            ts_v = torch.stack([t.reshape(()) for t in ts]) if isinstance(ts, (list, tuple)) else ts
+            z = self._draw_gamma_z(self._gamma.dtype)
+            zs = torch.clip(z, (-tau / zo_eps) * ts_v, (tau / zo_eps) * ts_v)
+        self._set_gamma(self._gamma + delta * zs * zo_eps)
+        return zs
+
+    def _loss(self, model, x):
+        return forward_wrap_with_option_len(model, **x, return_dict=True).loss
+
+    def zo_forward(self, new=None, pre_trained=None, x=None, apply=False):
+        """trainer.py:564-614: one SPSA iteration on gamma (apply=False), or the final
+        apply_constraints with the current gamma (apply=True)."""
+        if apply:
+            self.apply_constraints(new, pre_trained, iter(self.constraints), apply=True)
+            return
+        with torch.no_grad():
+            tab = self._table(new, pre_trained)
+            trusted = self._in_event and self._norms is not None
+            ts_v = self._norms if trusted else self._group_norms(tab)
+            ts_v = ts_v.clone()
+            if self.init:
+                self._set_gamma(ts_v.clone())
+            zs = self.perturb_gamma(1, ts=ts_v, tau=TAU, zo_eps=GAMMA_EPS)
+            self._freeze(new)
+            self._apply_alpha(tab, self._ratio(ts_v))
+            loss1 = self._loss(new, x)
+            n1 = self._reverse(tab)
+            self.perturb_gamma(-2, ts=ts_v, zs=zs, tau=TAU, zo_eps=GAMMA_EPS)
+            self._apply_alpha(tab, self._ratio(n1))
+            loss2 = self._loss(new, x)
+            self._reverse(tab)
+            self.perturb_gamma(1, ts=ts_v, zs=zs, tau=TAU, zo_eps=GAMMA_EPS)
+            grad = (loss1 - loss2) / (2 * GAMMA_EPS)
+            new_gamma = torch.clip(self._gamma - STEP_SIZE * ts_v * grad * zs, (1 - TAU) * ts_v, (1 + TAU) * ts_v)
+            self._set_gamma(new_gamma)
+        self.ts = [ts_v[i] for i in range(self.G)]
+        self.last_losses = (loss1, loss2)
+
+    def forward(self, new=None, pre_trained=None, x=None, apply=False):
+        """trainer.py:714-741 (first-order gamma objective)."""
+        raise NotImplementedError("DiZO first-order objective (ENHANCED=fo) is not implemented yet")
+
+    def close(self) -> None:
+        if self._tab is not None:
+            self._tab.close()
+            self._tab = None
+
+
+class dizo_trainer:  # noqa: N801 (reference name)
+    """Driver of the DiZO event (trainer.py:744-830)."""
+
+    def __init__(self, base_model, pgmloader, norm_mode, proj_lr, max_iters, exclude_list=[]) -> None:  # noqa: B006
+        self.proj_lr = proj_lr
+        self.max_iters = max_iters
+        self.exclude_list = exclude_list
+        self.dizo = DiZO(base_model, norm_mode=norm_mode, exclude_list=exclude_list)
+        self.device = self.dizo._device
+        self.pre_trained = base_model
+        self.pgm_optimizer = torch.optim.Adam(self.dizo.parameters(), lr=self.proj_lr)
+        self.pgmloader = pgmloader
+        self.dataset_iterator = iter(self.pgmloader) if pgmloader is not None else None
+        self.criterion = torch.nn.CrossEntropyLoss()
+        self.i = 0
+        self.gamma_seed = 0
+
+    def bind_model(self, model) -> None:
+        """Registers the projection table of (model, anchor) ahead of the first event."""
+        self.dizo._table(model, self.pre_trained)
+
+    def _next_batch(self):
+        if self.pgmloader is None:
+            raise DzError("dizo_trainer: no data loader for the gamma search")
+        try:
+            data = next(self.dataset_iterator)
+        except StopIteration:
+            self.dataset_iterator = iter(self.pgmloader)
+            data = next(self.dataset_iterator)
+        return {k: (v.to(self.device) if torch.is_tensor(v) else v) for k, v in data.items()}
+
+    def dizo_zo_iters(self, model, base_model, apply=False):
+        """trainer.py:782-803: max_iters SPSA iterations on gamma, then the final apply."""
+        dz = self.dizo
+        dz.gamma_seed = self.gamma_seed
+        dz._draws = 0
+        dz._norms = None
+        dz._in_event = True  # between the passes below nothing else writes theta
+        try:
+            if not apply:
+                self.count = 0
+                dz.init = True
+                while self.count < self.max_iters:
+                    data = self._next_batch()
+                    dz.zo_forward(model, base_model, x=data)
+                    dz.init = False
+                    self.count += 1
+            dz.zo_forward(model, self.pre_trained, apply=True)
+        finally:
+            dz._in_event = False
+            dz._norms = None
+        self.i += 1
+
+    def dizo_iters(self, model, base_model, apply=False):
+        """trainer.py:805-830 (first-order gamma search)."""
+        raise NotImplementedError("DiZO first-order gamma search (ENHANCED=fo) is not implemented yet")
+
+    def close(self) -> None:
+        self.dizo.close()

@@ -165,6 +165,8 @@ class ProjTable(_Table):
 
     def __init__(self, tensors: Sequence[torch.Tensor], anchors: Sequence[torch.Tensor]):
         super().__init__(tensors, anchors, None, "ProjTable")
+        # bytes of one read (or write) of every registered tensor
+        self.bytes_per_tensor_pass = sum(n * tensors[0].element_size() for n in self.numels)
 
     def _outs(self, sumsq, norm_f32, norm_T):
         for name, t, dt in (("sumsq", sumsq, torch.float64), ("norm_f32", norm_f32, torch.float32),

@@ -1,0 +1,391 @@
+"""Drop-in zeroth-order (MeZO) step of the reference trainer, on the HIP kernels.
+
+``ZOTrainerMixin`` carries the reference's ZO surface with unchanged
+signatures and attributes (luozoupi/DiZO, large_models/trainer.py):
+
+  zo_perturb_parameters(random_seed=None, scaling_factor=1)   trainer.py:1429-1444
+  forward_wrap_with_option_len(model, input_ids, ...)         trainer.py:1446-1522
+  zo_forward(model, inputs)                                   trainer.py:1524-1542
+  zo_step(model, inputs)                                      trainer.py:1570-1595
+  zo_update(args, model)                                      trainer.py:1597-1617
+
+plus ``zo_setup`` for the per-run set-up the reference does inside its training
+loop (ZO LambdaLR, trainer.py:1099-1101; trainable set, exclude list and the
+DiZO anchor, trainer.py:1147-1171). It can be mixed into a
+``transformers.Trainer`` subclass exactly where the reference defines these
+methods; ``ZOTrainer`` is a self-contained host that keeps the reference's
+per-step contract (trainer.py:1206-1326) without the HF Trainer machinery.
+
+What differs from the reference, by design:
+  * z is never materialised: every pass regenerates it from (seed, element
+    index) inside the kernel, so ``random_vector`` (trainer.py:1444) stays
+    empty (``export_z`` returns a tensor's z on demand);
+  * parameters are updated in place (the reference rebinds ``param.data``),
+    so the device tables of parameter addresses stay valid; a rebinding by
+    user code is detected and the tables are rebuilt;
+  * the restore pass that ends ``zo_step`` is deferred and fused with the
+    update pass of ``zo_update`` (one read-modify-write instead of two, with
+    the same per-element arithmetic). Any forward of the model, any
+    perturbation and ``zo_flush()`` apply a pending restore first, so the
+    parameters a caller can observe are the reference's;
+  * ``torch.normal`` z (torch's Philox + Box-Muller) is replaced by the
+    library's z: Philox4x32-10 keyed by the seed, 16 bits per element mapped
+    through a 15-bit normal quantile table. Seeds, scaling factors, rounding
+    and the update formula are the reference's.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from types import SimpleNamespace
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+from torch.nn import CrossEntropyLoss
+
+from ._lib import DzError
+from .table import ZOTable
+
+EMBED_TOKENS = "model.decoder.embed_tokens.weight"
+PROJECTED_SUFFIXES = ("self_attn.k_proj.weight", "self_attn.v_proj.weight")
+DIZO_INTERVAL = 50  # trainer.py:1611
+
+
+@dataclass
+class ZOArguments:
+    """The fields of the reference's OurArguments / TrainingArguments that the
+    ZO step reads (run.py:35-118; defaults of dizo.sh where it sets them)."""
+
+    learning_rate: float = 1e-7
+    zo_eps: float = 1e-3
+    max_steps: int = 20000
+    enhanced: Optional[str] = None  # None | "zo" | "fo" (dizo.sh passes the string "None")
+    gradient_accumulation_steps: int = 1
+    non_diff: bool = False
+    n_gpu: int = 1
+    logging_nan_inf_filter: bool = True
+    seed: int = 26
+    # build-specific: fuse the restore of zo_step with the update of zo_update
+    zo_fuse_restore: bool = True
+
+
+def layout_z_offsets(numels: Sequence[int]) -> List[int]:
+    """Global z index of each tensor's first element: tensors laid end to end in
+    named_parameters_to_optim order, each rounded up to 8 elements."""
+    offs, z = [], 0
+    for n in numels:
+        offs.append(z)
+        z += (int(n) + 7) // 8 * 8
+    return offs
+
+
+def select_trainable(model: torch.nn.Module) -> Tuple[List[Tuple[str, torch.nn.Parameter]], List[str]]:
+    """named_parameters_to_optim and exclude_list as trainer.py:1147-1160 builds them.
+
+    The ZO set is every parameter with requires_grad, minus the token
+    embedding when it comes first (OPT); the projected (DiZO) set is the
+    k_proj / v_proj weights; everything else is in exclude_list.
+    """
+    named = [(n, p) for n, p in model.named_parameters() if p.requires_grad]
+    if not named:
+        raise DzError("model has no parameters with requires_grad")
+    if named[0][0] != EMBED_TOKENS:
+        exclude = [k for k in model.state_dict().keys() if "lora" not in k]
+    else:
+        exclude = [EMBED_TOKENS] + [n for n, _ in named if not n.endswith(PROJECTED_SUFFIXES)]
+        named = named[1:]
+    return named, exclude
+
+
+def forward_wrap_with_option_len(self, input_ids=None, labels=None, option_len=None, num_options=None,
+                                 return_dict=None, **kwargs):
+    """The option-masked classification loss of trainer.py:1446-1522 (``self`` is the model).
+
+    Same torch operations in the same order, so the loss (in the model dtype)
+    is the reference's for the same logits. The per-example masking loop of
+    trainer.py:1473-1475 is written as one vectorised mask (positions before
+    the last option_len tokens), which sets the same elements.
+    """
+    with torch.no_grad():
+        outputs = self.forward(input_ids=input_ids, **kwargs)
+    if labels is None:
+        return outputs
+    logits = outputs.logits
+    shift_logits = logits[..., :-1, :].contiguous()
+    shift_labels = torch.clone(input_ids)[..., 1:].contiguous()
+    shift_labels[shift_labels == self.config.pad_token_id] = -100
+    if option_len is not None:
+        ol = torch.as_tensor(option_len, device=shift_labels.device).reshape(-1, 1)
+        pos = torch.arange(shift_labels.shape[1], device=shift_labels.device).reshape(1, -1)
+        shift_labels[pos < shift_labels.shape[1] - ol] = -100
+    loss_fct = CrossEntropyLoss(ignore_index=-100)
+    if num_options is not None:
+        log_probs = F.log_softmax(shift_logits, dim=-1)
+        mask = shift_labels != -100
+        shift_labels[~mask] = 0
+        selected = torch.gather(log_probs, dim=-1, index=shift_labels.unsqueeze(-1)).squeeze(-1)
+        selected = (selected * mask).sum(-1) / mask.sum(-1)
+        nopt = [int(x) for x in num_options]
+        if any(x != nopt[0] for x in nopt):
+            loss, start, count = 0, 0, 0
+            while start < len(nopt):
+                end = start + nopt[start]
+                loss = loss_fct(selected[start:end].unsqueeze(0), labels[start:end][0].unsqueeze(0)) + loss
+                count += 1
+                start = end
+            loss = loss / count
+        else:
+            selected = selected.view(-1, nopt[0])
+            loss = loss_fct(selected, labels.view(-1, nopt[0])[:, 0])
+    else:
+        loss = loss_fct(shift_logits.view(-1, self.config.vocab_size), shift_labels.view(-1))
+    if not return_dict:
+        return (loss, logits) + tuple(outputs[1:])
+    return SimpleNamespace(loss=loss)
+
+
+class _ZOTables:
+    """One ZOTable per dtype present in named_parameters_to_optim, sharing one
+    global z layout (so z does not depend on how dtypes are grouped)."""
+
+    def __init__(self, named: Sequence[Tuple[str, torch.nn.Parameter]]):
+        self.names = [n for n, _ in named]
+        self.params = [p for _, p in named]
+        self.z_offsets = layout_z_offsets([p.numel() for p in self.params])
+        self._ptrs = [p.data_ptr() for p in self.params]
+        groups: Dict[torch.dtype, List[int]] = {}
+        for i, p in enumerate(self.params):
+            groups.setdefault(p.dtype, []).append(i)
+        self.tables: List[Tuple[ZOTable, List[int]]] = []
+        for idx in groups.values():
+            tab = ZOTable([self.params[i].data for i in idx], z_offsets=[self.z_offsets[i] for i in idx])
+            self.tables.append((tab, idx))
+        self.bytes_per_pass = sum(2 * p.numel() * p.element_size() for p in self.params)
+
+    def stale(self) -> bool:
+        return any(p.data_ptr() != q for p, q in zip(self.params, self._ptrs))
+
+    def close(self):
+        for tab, _ in self.tables:
+            tab.close()
+        self.tables = []
+
+
+class ZOTrainerMixin:
+    """The reference's ZO step methods, running on the library's kernels.
+
+    Expects ``self.args`` (ZOArguments fields), ``self.state.global_step``,
+    ``self.lr_scheduler`` and ``self._get_learning_rate()`` as on an HF
+    Trainer; ``zo_setup`` provides all of them when absent.
+    """
+
+    forward_wrap_with_option_len = staticmethod(forward_wrap_with_option_len)
+
+    # ------------------------------------------------------------ set-up --
+    def zo_setup(self, model: torch.nn.Module, train_dataloader=None, *, base_model=None,
+                 optimizer: Optional[torch.optim.Optimizer] = None) -> None:
+        """trainer.py:1099-1101 (ZO LambdaLR) and trainer.py:1147-1171 (trainable
+        set, exclude list, DiZO anchor and driver)."""
+        from .dizo import dizo_trainer
+
+        args = self.args
+        self.model = model
+        if not hasattr(self, "state"):
+            self.state = SimpleNamespace(global_step=0)
+        if optimizer is None:
+            # the ZO path reads only the learning rate of the optimizer's group
+            optimizer = torch.optim.SGD([torch.zeros(1, requires_grad=True)], lr=args.learning_rate)
+        self.optimizer = optimizer
+        self.lr_scheduler = torch.optim.lr_scheduler.LambdaLR(
+            optimizer, lambda step: 1 - self.state.global_step / (2 * args.max_steps))
+        self.named_parameters_to_optim, self.exclude_list = select_trainable(model)
+        if args.enhanced in ("zo", "fo"):
+            if base_model is None:
+                base_model = _anchor_copy(model, self.exclude_list)
+            self.base_model = base_model
+            self.dizo_trainer = dizo_trainer(base_model, train_dataloader, "l2norm", 0.1, 10, self.exclude_list)
+            self.dizo_trainer.bind_model(model)
+        else:
+            args.enhanced = None
+        self.loss_list = []
+        self.random_vector = {}
+        self.zo_random_seed = None
+        self.projected_grad = None
+        self._zo_tabs = None
+        self._pending_restore = None
+        self.kernel_timer = None
+        self._hook = model.register_forward_pre_hook(lambda m, a: self.zo_flush())
+
+    def _get_learning_rate(self) -> float:
+        return self.lr_scheduler.get_last_lr()[0]
+
+    def _zo_tables(self) -> _ZOTables:
+        tabs = self._zo_tabs
+        if tabs is None or tabs.stale():
+            if tabs is not None:
+                tabs.close()
+            tabs = self._zo_tabs = _ZOTables(self.named_parameters_to_optim)
+        return tabs
+
+    def _launch(self, what: str, fn, tabs: _ZOTables) -> None:
+        timer = self.kernel_timer
+        if timer is None:
+            for tab, _ in tabs.tables:
+                fn(tab)
+        else:
+            with timer.span(what, tabs.bytes_per_pass):
+                for tab, _ in tabs.tables:
+                    fn(tab)
+
+    # -------------------------------------------------------------- step --
+    def zo_flush(self) -> None:
+        """Applies a deferred restore (the +1 perturbation that ends zo_step)."""
+        pending = self._pending_restore
+        if pending is not None:
+            self._pending_restore = None
+            seed, eps = pending
+            tabs = self._zo_tables()
+            self._launch("perturb", lambda t: t.perturb(seed, 1.0, eps), tabs)
+
+    def zo_perturb_parameters(self, random_seed=None, scaling_factor=1):
+        """trainer.py:1429-1444: theta <- theta + scaling_factor * z * zo_eps, in place."""
+        self.zo_flush()
+        seed = random_seed if random_seed is not None else self.zo_random_seed
+        torch.manual_seed(seed)  # the reference re-seeds torch's generators here
+        tabs = self._zo_tables()
+        eps = float(self.args.zo_eps)
+        s = float(scaling_factor)
+        self._launch("perturb", lambda t: t.perturb(seed, s, eps), tabs)
+
+    def _prepare_inputs(self, inputs):
+        dev = self.named_parameters_to_optim[0][1].device
+        return {k: (v.to(dev, non_blocking=True) if torch.is_tensor(v) else v) for k, v in inputs.items()}
+
+    def zo_forward(self, model, inputs):
+        """trainer.py:1524-1542."""
+        model.eval()
+        if self.args.non_diff:
+            raise NotImplementedError("the non-differentiable (SQuAD F1) objective is not part of this library")
+        with torch.inference_mode():
+            inputs = self._prepare_inputs(inputs)
+            loss = self.forward_wrap_with_option_len(model, **inputs, return_dict=True).loss
+            if self.args.n_gpu > 1:
+                loss = loss.mean()
+        return loss.detach()
+
+    def zo_step(self, model, inputs):
+        """trainer.py:1570-1595. Returns loss1; sets zo_random_seed and projected_grad."""
+        args = self.args
+        self.zo_random_seed = np.random.randint(1000000000)
+        self.zo_perturb_parameters(scaling_factor=1)
+        loss1 = self.zo_forward(model, inputs)
+        self.zo_perturb_parameters(scaling_factor=-2)
+        loss2 = self.zo_forward(model, inputs)
+        self.projected_grad = ((loss1 - loss2) / (2 * self.args.zo_eps)).item()
+        assert self.args.gradient_accumulation_steps == 1
+        if args.zo_fuse_restore:
+            self._pending_restore = (self.zo_random_seed, float(args.zo_eps))
+        else:
+            self.zo_perturb_parameters(scaling_factor=1)
+        return loss1
+
+    def zo_update(self, args, model):
+        """trainer.py:1597-1617: theta <- theta - lr * (projected_grad * z), the
+        DiZO event every 50 steps, then the scheduler step."""
+        seed = self.zo_random_seed
+        torch.manual_seed(seed)
+        tabs = self._zo_tables()
+        g, lr = float(self.projected_grad), float(self._get_learning_rate())
+        pending = self._pending_restore
+        if pending is not None and pending[0] == seed:
+            self._pending_restore = None
+            eps = pending[1]
+            self._launch("restore_update", lambda t: t.restore_update(seed, eps, g, lr), tabs)
+        else:
+            self.zo_flush()
+            self._launch("update", lambda t: t.update(seed, g, lr), tabs)
+        if (self.state.global_step + 1) % DIZO_INTERVAL == 0 and args.enhanced:
+            self.dizo_trainer.gamma_seed = seed
+            if args.enhanced == "zo":
+                self.dizo_trainer.dizo_zo_iters(model, base_model=self.base_model)
+            else:
+                self.dizo_trainer.dizo_iters(model, base_model=self.base_model)
+        self.lr_scheduler.step()
+
+    def export_z(self, name: str, seed: Optional[int] = None) -> torch.Tensor:
+        """The z that seed (default: the current zo_random_seed) applies to
+        parameter `name` (what the reference would hold in random_vector[name])."""
+        tabs = self._zo_tables()
+        i = tabs.names.index(name)
+        seed = self.zo_random_seed if seed is None else seed
+        for tab, idx in tabs.tables:
+            if i in idx:
+                return tab.export_z(int(seed), idx.index(i))
+        raise KeyError(name)
+
+    def zo_close(self) -> None:
+        self.zo_flush()
+        if self._zo_tabs is not None:
+            self._zo_tabs.close()
+            self._zo_tabs = None
+        if getattr(self, "dizo_trainer", None) is not None:
+            self.dizo_trainer.close()
+        if getattr(self, "_hook", None) is not None:
+            self._hook.remove()
+            self._hook = None
+
+
+def _anchor_copy(model: torch.nn.Module, exclude_list: Sequence[str]) -> torch.nn.Module:
+    """theta0 as the reference keeps it (trainer.py:1163-1167): a copy of the
+    model whose excluded (non-projected) tensors live on the CPU. Only the
+    projected tensors are copied on the device here; the rest are CPU copies."""
+    import copy
+
+    excl = set(exclude_list)
+    memo = {}
+    for name, p in model.named_parameters():
+        if name in excl:
+            memo[id(p)] = torch.nn.Parameter(p.detach().to("cpu", copy=True), requires_grad=p.requires_grad)
+    base = copy.deepcopy(model, memo)
+    return base
+
+
+class ZOTrainer(ZOTrainerMixin):
+    """Minimal host of the ZO step: the reference's per-step contract
+    (trainer.py:1206-1326) without the HF Trainer (no evaluation, saving or
+    callbacks): zo_step, the NaN/inf loss filter, zo_update, global_step += 1,
+    a loss record every step and a log line every 50 steps."""
+
+    def __init__(self, model, args: ZOArguments, train_dataloader=None, *, base_model=None):
+        self.args = args
+        self.state = SimpleNamespace(global_step=0, epoch=0.0, log_history=[])
+        self.zo_setup(model, train_dataloader, base_model=base_model)
+        self.tr_loss = torch.zeros((), device=self.named_parameters_to_optim[0][1].device)
+        self._last_logged = 0
+
+    def training_step(self, inputs) -> torch.Tensor:
+        """One optimisation step (trainer.py:1224-1326 with gradient_accumulation_steps = 1)."""
+        model = self.model
+        tr_loss_step = self.zo_step(model, inputs)
+        if self.args.logging_nan_inf_filter and (torch.isnan(tr_loss_step) or torch.isinf(tr_loss_step)):
+            self.tr_loss += self.tr_loss / (1 + self.state.global_step - self._last_logged)
+        else:
+            self.tr_loss += tr_loss_step
+        self.zo_update(self.args, model)
+        self.state.global_step += 1
+        if self.state.global_step % DIZO_INTERVAL == 0:
+            self.state.log_history.append({"loss": round(tr_loss_step.item(), 4),
+                                           "lr": self._get_learning_rate(),
+                                           "step": self.state.global_step})
+        self.loss_list.append(tr_loss_step)
+        return tr_loss_step
+
+    def train(self, batches, max_steps: Optional[int] = None):
+        n = max_steps if max_steps is not None else self.args.max_steps
+        it = iter(batches)
+        for _ in range(n):
+            self.training_step(next(it))
+        self.zo_flush()
+        return [float(x) for x in self.loss_list]

@@ -53,19 +53,21 @@ def projected_grad(loss1: torch.Tensor, loss2: torch.Tensor, zo_eps: float) -> f
     return ((loss1 - loss2) / (2 * zo_eps)).item()
 
 
-def project_ratio(new: torch.Tensor, anchor: torch.Tensor, constraint: torch.Tensor) -> torch.Tensor:
-    """trainer.py:453-465 (l2norm mode)."""
+def project_ratio(new: torch.Tensor, anchor: torch.Tensor, constraint: torch.Tensor,
+                  norm: Callable = torch.norm) -> torch.Tensor:
+    """trainer.py:453-465 (l2norm mode). `norm` is torch.norm in the reference;
+    tests may inject another evaluation of the same norm."""
     t = new.detach() - anchor.detach()
-    norms = torch.norm(t)
+    norms = norm(t)
     return constraint / (norms + 1e-8)
 
 
 def apply_constraints(news: Sequence[torch.Tensor], anchors: Sequence[torch.Tensor],
-                      constraints: Sequence[torch.Tensor]) -> list:
+                      constraints: Sequence[torch.Tensor], norm: Callable = torch.norm) -> list:
     """trainer.py:405-436 over the projected tensors; returns the alphas."""
     alphas = []
     for new_para, anchor_para, c in zip(news, anchors, constraints):
-        alpha = project_ratio(new_para, anchor_para, c)
+        alpha = project_ratio(new_para, anchor_para, c, norm)
         alphas.append(alpha)
         v = (new_para.detach() - anchor_para.detach()) * alpha
         temp = v + anchor_para.detach()
@@ -85,7 +87,7 @@ def reverse_constraints(news: Sequence[torch.Tensor], anchors: Sequence[torch.Te
 
 
 def dizo_zo_iteration(news, anchors, gammas: list, init: bool, z_gamma: Sequence[torch.Tensor],
-                      loss_fn: Callable[[int], torch.Tensor]):
+                      loss_fn: Callable[[int], torch.Tensor], norm: Callable = torch.norm):
     """One ZO gamma iteration, trainer.py:564-614, with the gamma noise and the
     two losses supplied (loss_fn(k) is the k-th forward's loss, k = 0, 1).
 
@@ -93,7 +95,7 @@ def dizo_zo_iteration(news, anchors, gammas: list, init: bool, z_gamma: Sequence
     Returns (ts, loss1, loss2).
     """
     with torch.no_grad():
-        ts = [torch.norm(p.data - a.data) for p, a in zip(news, anchors)]
+        ts = [norm(p.data - a.data) for p, a in zip(news, anchors)]
         if init:
             for i in range(len(gammas)):
                 gammas[i] = ts[i]
@@ -103,12 +105,12 @@ def dizo_zo_iteration(news, anchors, gammas: list, init: bool, z_gamma: Sequence
             z = torch.clip(z_gamma[i], (-tau / zo_eps) * ts[i], (tau / zo_eps) * ts[i])
             zs.append(z)
             gammas[i] = gammas[i] + 1 * z * zo_eps
-        alphas = apply_constraints(news, anchors, gammas)
+        alphas = apply_constraints(news, anchors, gammas, norm)
         loss1 = loss_fn(0)
         reverse_constraints(news, anchors, alphas)
         for i in range(len(gammas)):
             gammas[i] = gammas[i] + -2 * zs[i] * zo_eps
-        alphas = apply_constraints(news, anchors, gammas)
+        alphas = apply_constraints(news, anchors, gammas, norm)
         loss2 = loss_fn(1)
         reverse_constraints(news, anchors, alphas)
         for i in range(len(gammas)):

@@ -1,0 +1,156 @@
+"""GPU parity of the drop-in ZO trainer and DiZO event (dizo_amd.trainer / dizo_amd.dizo).
+
+Two identical random-init OPT models: one steps through the library (kernels,
+fused restore+update, projection passes), the other through the reference's
+expressions (oracle.ref_torch, trainer.py:1429-1617 and 545-614) run by ROCm
+torch, fed the z the library exports and the library's gamma noise. The
+parameters, losses and gammas must agree bit for bit. The reference-side
+norm is torch's evaluation of the library's norm definition (fp64 sum of
+squares, correctly rounded fp32 sqrt, rounded to T); torch.norm itself is
+within one unit in the last place of it (tests/test_gpu_projection.py).
+"""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import arith as A
+from oracle import ref_torch as R
+
+pytestmark = pytest.mark.gpu
+
+DTS = [torch.float16, torch.bfloat16, torch.float32]
+
+
+def _lib_norm(t: torch.Tensor) -> torch.Tensor:
+    s = (t.double() ** 2).sum().float()
+    return torch.sqrt(s.double()).float().to(t.dtype)
+
+
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().contiguous().view({2: torch.int16, 4: torch.int32}[t.element_size()])
+
+
+def _same(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return a.dtype == b.dtype and a.shape == b.shape and torch.equal(_bits(a), _bits(b))
+
+
+def _ref_forward(model, batch):
+    from dizo_amd.trainer import forward_wrap_with_option_len
+    model.eval()
+    with torch.inference_mode():
+        return forward_wrap_with_option_len(model, **batch, return_dict=True).loss.detach()
+
+
+def _setup(dt, seed=3):
+    from dizo_amd.synth import build_opt, make_batches
+    model_a = build_opt("opt-tiny", dt, "cuda", seed=seed)
+    model_b = copy.deepcopy(model_a)
+    batches = make_batches(6, 4, 512, seed=5, device="cuda", min_len=8, max_len=20)
+    return model_a, model_b, batches
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("fuse", [True, False])
+def test_zo_steps_match_reference(dt, fuse):
+    from dizo_amd.trainer import ZOArguments, ZOTrainer, select_trainable
+    model_a, model_b, batches = _setup(dt)
+    steps, lr0, eps = 5, 1e-3, 1e-3
+    args = ZOArguments(learning_rate=lr0, zo_eps=eps, max_steps=steps, enhanced=None, zo_fuse_restore=fuse)
+    np.random.seed(26)
+    tr = ZOTrainer(model_a, args)
+    losses_a = [tr.training_step(batches[k]) for k in range(steps)]
+    tr.zo_flush()
+
+    np.random.seed(26)
+    named_b, _ = select_trainable(model_b)
+    names = [n for n, _ in named_b]
+    params_b = [p for _, p in named_b]
+    for k in range(steps):
+        seed = np.random.randint(1000000000)
+        zs = [tr.export_z(n, seed) for n in names]
+        R.zo_perturb_parameters(params_b, zs, 1, eps)
+        l1 = _ref_forward(model_b, batches[k])
+        R.zo_perturb_parameters(params_b, zs, -2, eps)
+        l2 = _ref_forward(model_b, batches[k])
+        g = R.projected_grad(l1, l2, eps)
+        R.zo_perturb_parameters(params_b, zs, 1, eps)
+        R.zo_update(params_b, zs, g, A.zo_lr(lr0, k, steps))
+        assert _same(losses_a[k], l1), f"step {k}: loss {losses_a[k]} vs {l1}"
+    pa = dict(model_a.named_parameters())
+    bad = [n for n, p in zip(names, params_b) if not _same(pa[n].data, p.data)]
+    assert not bad, f"{len(bad)} parameters differ after {steps} steps, e.g. {bad[:3]}"
+    tr.zo_close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_dizo_event_matches_reference(dt):
+    """dizo_trainer.dizo_zo_iters (10 SPSA iterations on gamma + final apply)."""
+    from dizo_amd import _lib as L
+    from dizo_amd.dizo import dizo_trainer
+    from dizo_amd.synth import Cycle
+    from dizo_amd.table import normals
+    from dizo_amd.trainer import select_trainable
+    model_a, model_b, batches = _setup(dt, seed=11)
+    anchor_a, anchor_b = copy.deepcopy(model_a), copy.deepcopy(model_b)
+    # move theta away from theta0 identically on both models
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    with torch.no_grad():
+        for pa, pb in zip(model_a.parameters(), model_b.parameters()):
+            noise = (torch.randn(pa.shape, device="cuda", generator=gen) * 1e-2).to(dt)
+            pa.add_(noise)
+            pb.add_(noise)
+    _, exclude = select_trainable(model_a)
+    dtr = dizo_trainer(anchor_a, Cycle(batches), "l2norm", 0.1, 10, exclude)
+    dtr.gamma_seed = 4242
+    dtr.dizo_zo_iters(model_a, base_model=anchor_a)
+
+    names = dtr.dizo.constraints_name
+    G = len(names)
+    pb = dict(model_b.named_parameters())
+    p0 = dict(anchor_b.named_parameters())
+    news = [pb[n] for n in names]
+    anchors = [p0[n] for n in names]
+    gammas = [torch.nn.Parameter(torch.Tensor([0]).cuda()) for _ in range(G)]
+    for it in range(10):
+        zg = normals(4242, L.DZ_STREAM_GAMMA, it * G, G, dt, torch.device("cuda", 0))
+        data = batches[it % len(batches)]
+        R.dizo_zo_iteration(news, anchors, gammas, it == 0, [zg[i:i + 1] for i in range(G)],
+                            lambda k: _ref_forward(model_b, data), norm=_lib_norm)
+    R.apply_constraints(news, anchors, gammas, norm=_lib_norm)
+    g_ref = torch.cat([g.reshape(1) for g in gammas])
+    assert _same(dtr.dizo.gamma(), g_ref), f"gamma {dtr.dizo.gamma()} vs {g_ref}"
+    pa = dict(model_a.named_parameters())
+    bad = [n for n in pb if not _same(pa[n].data, pb[n].data)]
+    assert not bad, f"{len(bad)} parameters differ after the DiZO event, e.g. {bad[:3]}"
+    dtr.close()
+
+
+def test_full_run_with_event_is_deterministic():
+    """60 steps with ENHANCED=zo (one DiZO event at global step 49) twice from the
+    same seeds give bit-identical parameters and losses; the event changes the
+    parameters relative to plain MeZO only from step 49 on (DiZO == MeZO before
+    the first projection, the invariant of the reference's logs)."""
+    from dizo_amd.synth import Cycle, build_opt, make_batches
+    from dizo_amd.trainer import ZOArguments, ZOTrainer
+
+    batches = make_batches(6, 4, 512, seed=9, device="cuda", min_len=8, max_len=20)
+
+    def run(enhanced, steps):
+        model = build_opt("opt-tiny", torch.float16, "cuda", seed=21)
+        args = ZOArguments(learning_rate=1e-3, zo_eps=1e-3, max_steps=60, enhanced=enhanced)
+        np.random.seed(26)
+        tr = ZOTrainer(model, args, train_dataloader=Cycle(batches))
+        it = iter(Cycle(batches))
+        losses = [float(tr.training_step(next(it))) for _ in range(steps)]
+        tr.zo_close()
+        return losses, [p.detach().clone() for p in model.parameters()]
+
+    l_dizo, p_dizo = run("zo", 60)
+    l_dizo2, p_dizo2 = run("zo", 60)
+    assert l_dizo == l_dizo2
+    assert all(_same(a, b) for a, b in zip(p_dizo, p_dizo2))
+    l_mezo, _ = run(None, 60)
+    assert l_mezo[:50] == l_dizo[:50]  # steps 0..49 use the same seeds and theta
+    assert l_mezo[50:] != l_dizo[50:]
