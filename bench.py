@@ -217,7 +217,15 @@ def kernel_microbench(wl_name: str, reps: int = 10, log=print):
         out[name] = {"ms": t, "GBps": nbytes / t / 1e6, "frac": nbytes / t / 1e6 / HBM_PEAK_GBPS}
         log(f"[kernels] {name:15s} {t:8.3f} ms {nbytes / t / 1e6:8.1f} GB/s")
     tabs.close()
-    return {"bytes_per_pass": nbytes, "passes": out}
+    # calibration for counter-based traffic: a plain device copy of known size
+    # (reads and writes copy_bytes each), launched twice
+    copy_bytes = 4 << 30
+    src = torch.empty(copy_bytes // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"bytes_per_pass": nbytes, "passes": out, "calibration_copy_bytes": copy_bytes}
 
 
 def main(argv=None):

@@ -35,7 +35,7 @@ What differs from the reference, by design:
 """
 from __future__ import annotations
 
-import math
+import warnings
 from dataclasses import dataclass
 from types import SimpleNamespace
 from typing import Dict, List, Optional, Sequence, Tuple
@@ -198,6 +198,8 @@ class ZOTrainerMixin:
             # the ZO path reads only the learning rate of the optimizer's group
             optimizer = torch.optim.SGD([torch.zeros(1, requires_grad=True)], lr=args.learning_rate)
         self.optimizer = optimizer
+        # the ZO path steps the scheduler without optimizer.step(), as the reference does
+        warnings.filterwarnings("ignore", message=r"Detected call of `lr_scheduler.step\(\)` before")
         self.lr_scheduler = torch.optim.lr_scheduler.LambdaLR(
             optimizer, lambda step: 1 - self.state.global_step / (2 * args.max_steps))
         self.named_parameters_to_optim, self.exclude_list = select_trainable(model)
@@ -266,12 +268,12 @@ class ZOTrainerMixin:
     def zo_forward(self, model, inputs):
         """trainer.py:1524-1542."""
         model.eval()
-        if self.args.non_diff:
+        if getattr(self.args, "non_diff", False):
             raise NotImplementedError("the non-differentiable (SQuAD F1) objective is not part of this library")
         with torch.inference_mode():
             inputs = self._prepare_inputs(inputs)
             loss = self.forward_wrap_with_option_len(model, **inputs, return_dict=True).loss
-            if self.args.n_gpu > 1:
+            if getattr(self.args, "n_gpu", 1) > 1:
                 loss = loss.mean()
         return loss.detach()
 
@@ -285,7 +287,7 @@ class ZOTrainerMixin:
         loss2 = self.zo_forward(model, inputs)
         self.projected_grad = ((loss1 - loss2) / (2 * self.args.zo_eps)).item()
         assert self.args.gradient_accumulation_steps == 1
-        if args.zo_fuse_restore:
+        if getattr(args, "zo_fuse_restore", True):
             self._pending_restore = (self.zo_random_seed, float(args.zo_eps))
         else:
             self.zo_perturb_parameters(scaling_factor=1)

@@ -81,7 +81,9 @@ int32_t dz_table_matches(const dz_table* t, const uint64_t* ptrs, int32_t n);
 int32_t dz_table_z_offset(const dz_table* t, int32_t idx, uint64_t* out);
 
 /* ---- ZO step (trainer.py:1429-1444, 1570-1617) -------------------------- */
-/* Optional device pointers (NULL = use the by-value argument):
+/* Launches on one table share its work counters: order them on one stream
+ * (never run two launches of the same table concurrently).
+ * Optional device pointers (NULL = use the by-value argument):
  *   d_seed: uint64 seed;  d_grad: projected_grad as one element of the table
  *   dtype;  d_lr: fp32 learning rate. They let a captured graph replay with
  *   new values. */
