@@ -237,6 +237,28 @@ __device__ __forceinline__ void st_stream(void* p, dz_u32x4 v) {
   __builtin_nontemporal_store(v, (dz_u32x4*)p);
 }
 
+// Wave-uniform copy of a 32-bit value in a scalar register.
+// __builtin_amdgcn_readfirstlane returns a signed int: cast back to uint32_t
+// before widening, or values >= 2^31 would sign-extend.
+__device__ __forceinline__ uint32_t rfl_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
+}
+__device__ __forceinline__ uint64_t rfl_u64(uint64_t x) {
+  return ((uint64_t)rfl_u32((uint32_t)(x >> 32)) << 32) | (uint64_t)rfl_u32((uint32_t)x);
+}
+
+// A chunk descriptor read from LDS is the same for every lane: move it to
+// scalar registers so tile addresses are formed once per wave.
+__device__ __forceinline__ DzChunk uniform_chunk(const DzChunk& c) {
+  DzChunk u;
+  u.ptr = rfl_u64(c.ptr);
+  u.aux = 0;
+  u.zgroup = rfl_u64(c.zgroup);
+  u.n = rfl_u32(c.n);
+  u.meta = rfl_u32(c.meta);
+  return u;
+}
+
 // One tile of an RMW launch.
 template <int DT, int MODE>
 __device__ __forceinline__ void rmw_chunk(const DzChunk& ch, const typename RmwTraits<DT, MODE>::E* tab,
@@ -322,7 +344,8 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
   using E = typename Tr::E;
   using S = typename DT_<DT>::S;
   __shared__ __attribute__((aligned(16))) E tab[kDzTabEntries];
-  __shared__ uint32_t slot[2];
+  __shared__ uint32_t sidx[3];    // tile indices k, k+1, k+2 (>= nchunks: none)
+  __shared__ DzChunk sdesc[2];    // descriptors of tiles k, k+1
   const DzScalars sc = resolve_scalars<DT>(sc_in, sp);
   {
     const S* q = (const S*)qtab;
@@ -331,20 +354,57 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
   }
   // Counters in use: every one of them must be served by at least one
   // workgroup, or its tiles would never be taken (a small grid uses fewer).
-  const uint32_t ncnt = max(1u, min((uint32_t)kCounters, gridDim.x >> 3));
-  const uint32_t j = (blockIdx.x >> 3) % ncnt;
+  const uint32_t ncnt = rfl_u32(max(1u, min((uint32_t)kCounters, gridDim.x >> 3)));
+  const uint32_t j = rfl_u32((blockIdx.x >> 3) % ncnt);
   uint32_t* mine = counters + j * kCounterStride;
-  if (threadIdx.x == 0) slot[0] = atomicAdd(mine, 1u);
+  const uint64_t nch = nchunks;
+  // Two-deep pipeline kept by thread 0: while tile k streams, the index of
+  // tile k+2 is taken from the counter and the descriptor of tile k+1 is
+  // loaded, so neither latency sits between two tiles.
+  if (threadIdx.x == 0) {
+    const uint64_t c0 = (uint64_t)atomicAdd(mine, 1u) * ncnt + j;
+    const uint64_t c1 = (uint64_t)atomicAdd(mine, 1u) * ncnt + j;
+    sidx[0] = (uint32_t)min(c0, nch);
+    sidx[1] = (uint32_t)min(c1, nch);
+    if (c0 < nch) sdesc[0] = chunks[c0];
+  }
   __syncthreads();
-  uint32_t k = 0;
-  uint64_t c = (uint64_t)slot[0] * ncnt + j;
-  while (c < nchunks) {
-    if (threadIdx.x == 0) slot[(k + 1) & 1] = atomicAdd(mine, 1u);
-    const uint32_t cu = __builtin_amdgcn_readfirstlane((uint32_t)c);
-    rmw_chunk<DT, MODE>(chunks[cu], tab, sc);
+  for (uint32_t k = 0;; ++k) {
+    const uint32_t c = sidx[k % 3];
+    if (c >= nchunks) break;
+    const DzChunk ch = uniform_chunk(sdesc[k & 1]);
+    // Wave 0 fetches the next descriptor with scalar loads (it is uniform,
+    // so it costs no vector registers); lane 0 takes the next index with a
+    // vector atomic. The anchor field is unused by ZO tables.
+    uint32_t grabbed = 0;
+    uint64_t n_ptr = 0, n_zg = 0;
+    uint32_t n_n = 0, n_meta = 0;
+    bool have_next = false;
+    if ((rfl_u32(threadIdx.x) >> 6) == 0) {  // wave 0 (uniform branch)
+      if (threadIdx.x == 0) grabbed = atomicAdd(mine, 1u);
+      const uint32_t cn = rfl_u32(sidx[(k + 1) % 3]);
+      if (cn < nchunks) {
+        const DzChunk* src = chunks + cn;
+        n_ptr = src->ptr;
+        n_zg = src->zgroup;
+        n_n = src->n;
+        n_meta = src->meta;
+        have_next = true;
+      }
+    }
+    rmw_chunk<DT, MODE>(ch, tab, sc);
+    if (threadIdx.x == 0) {
+      sidx[(k + 2) % 3] = (uint32_t)min((uint64_t)grabbed * ncnt + j, nch);
+      if (have_next) {
+        DzChunk& d = sdesc[(k + 1) & 1];
+        d.ptr = n_ptr;
+        d.aux = 0;
+        d.zgroup = n_zg;
+        d.n = n_n;
+        d.meta = n_meta;
+      }
+    }
     __syncthreads();
-    ++k;
-    c = (uint64_t)slot[k & 1] * ncnt + j;
   }
   if (threadIdx.x == 0) {
     const uint32_t done = atomicAdd(counters + kCounters * kCounterStride, 1u);

@@ -106,8 +106,12 @@ def forward_wrap_with_option_len(self, input_ids=None, labels=None, option_len=N
     Same torch operations in the same order, so the loss (in the model dtype)
     is the reference's for the same logits. The per-example masking loop of
     trainer.py:1473-1475 is written as one vectorised mask (positions before
-    the last option_len tokens), which sets the same elements.
+    the last option_len tokens), which sets the same elements. The forward
+    runs without a key/value cache (use_cache=False unless the caller says
+    otherwise): a loss never reads it, and building it costs two
+    concatenations per layer; the logits are the same.
     """
+    kwargs.setdefault("use_cache", False)
     with torch.no_grad():
         outputs = self.forward(input_ids=input_ids, **kwargs)
     if labels is None:

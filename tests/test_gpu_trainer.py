@@ -154,3 +154,19 @@ def test_full_run_with_event_is_deterministic():
     l_mezo, _ = run(None, 60)
     assert l_mezo[:50] == l_dizo[:50]  # steps 0..49 use the same seeds and theta
     assert l_mezo[50:] != l_dizo[50:]
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_loss_forward_without_kv_cache_is_identical(dt):
+    """On the device too: the loss forward's use_cache=False leaves logits and loss unchanged."""
+    from dizo_amd.synth import build_opt, make_batches
+    from dizo_amd.trainer import forward_wrap_with_option_len
+    model = build_opt("opt-mini", dt, "cuda", seed=2)
+    b = make_batches(1, 8, 4096, seed=3, device="cuda", min_len=20, max_len=40)[0]
+    with torch.inference_mode():
+        a = forward_wrap_with_option_len(model, **b, return_dict=True).loss
+        c = forward_wrap_with_option_len(model, **b, use_cache=True, return_dict=True).loss
+        la = model(input_ids=b["input_ids"], attention_mask=b["attention_mask"], use_cache=False).logits
+        lc = model(input_ids=b["input_ids"], attention_mask=b["attention_mask"], use_cache=True).logits
+    assert _same(a, c)
+    assert _same(la, lc)

@@ -92,3 +92,18 @@ def test_bruteforce_closed_forms():
     assert loss == pytest.approx((np.log(8 / 7) + np.log(2)) / 2, abs=1e-9)
     ids[2, L - 1] = 1  # pad-id target: row 2 has no option token
     assert np.isnan(OL.row_scores(logits, ids, [1] * 4, pad_id=1)[2])
+
+
+def test_loss_without_kv_cache_is_identical(tiny_model):
+    """The loss forward skips HF's key/value cache; the logits and the loss are unchanged."""
+    from dizo_amd.synth import make_batch
+    from dizo_amd.trainer import forward_wrap_with_option_len
+
+    b = make_batch(4, 512, gen=torch.Generator().manual_seed(11), min_len=5, max_len=12)
+    with torch.no_grad():
+        a = forward_wrap_with_option_len(tiny_model, **b, return_dict=True).loss
+        c = forward_wrap_with_option_len(tiny_model, **b, use_cache=True, return_dict=True).loss
+        la = tiny_model(input_ids=b["input_ids"], attention_mask=b["attention_mask"], use_cache=False).logits
+        lc = tiny_model(input_ids=b["input_ids"], attention_mask=b["attention_mask"], use_cache=True).logits
+    assert torch.equal(a, c)
+    assert torch.equal(la, lc)
