@@ -199,6 +199,7 @@ def kernel_microbench(wl_name: str, reps: int = 10, log=print):
         "restore+1": lambda t: t.perturb(26, 1.0, 1e-3),
         "update": lambda t: t.update(26, g, 1e-6),
         "restore_update": lambda t: t.restore_update(26, 1e-3, g, 1e-6),
+        "restore_update_perturb": lambda t: t.restore_update_perturb(26, 27, 1e-3, g, 1e-6),
     }
     for name, fn in cases.items():
         for tab, _ in tabs.tables:
@@ -262,7 +263,7 @@ def main(argv=None):
     wl = WORKLOADS[a.workload]
     value = a.steps / r["elapsed"]
     summ = r["summary"]
-    rmw = [summ[k] for k in ("perturb", "restore_update", "update") if k in summ]
+    rmw = [summ[k] for k in ("perturb", "restore_update", "update", "restore_update_perturb") if k in summ]
     rmw_bytes = sum(s["bytes_per_launch"] * s["launches"] for s in rmw)
     rmw_ms = sum(s["total_ms"] for s in rmw)
     rmw_launches = sum(s["launches"] for s in rmw)
@@ -287,7 +288,7 @@ def main(argv=None):
                    "zo_params": r["P"], "dizo_events_timed": r["events"], "global_batch": 2 * wl["batch"],
                    "seq_len": wl["fixed_len"] or wl["max_len"]},
         "roofline": {
-            "kernel": "rmw_kernel (perturb / fused restore+update)",
+            "kernel": "rmw_kernel (perturb -2 / restore+update / restore+update+next perturb)",
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBPS,

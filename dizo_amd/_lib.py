@@ -51,6 +51,7 @@ SIGNATURES = {
     "dz_perturb": (_i32, [_p, _u64, _f32, _f32, _p, _p]),
     "dz_update": (_i32, [_p, _u64, _f32, _f32, _p, _p, _p, _p]),
     "dz_restore_update": (_i32, [_p, _u64, _f32, _f32, _f32, _p, _p, _p, _p]),
+    "dz_restore_update_perturb": (_i32, [_p, _u64, _u64, _f32, _f32, _f32, _p, _p, _p, _p, _p]),
     "dz_normals": (_i32, [_u64, _u32, _u64, _i64, _i32, _p, _p]),
     "dz_export_z": (_i32, [_p, _u64, _i32, _p, _p]),
     "dz_philox": (_i32, [_u64, _u32, _u64, _i64, _p, _p]),
@@ -63,7 +64,9 @@ _lib = None
 
 
 def lib_path() -> str:
-    return LIB_PATH
+    """The library to load: dizo_amd/libdizo_amd.so, or $DIZO_AMD_LIB if set
+    (a variant built elsewhere, e.g. with other compile-time tile sizes)."""
+    return os.environ.get("DIZO_AMD_LIB") or LIB_PATH
 
 
 def load() -> C.CDLL:
@@ -73,11 +76,12 @@ def load() -> C.CDLL:
         return _lib
     with _lock:
         if _lib is None:
-            if not os.path.exists(LIB_PATH):
+            path = lib_path()
+            if not os.path.exists(path):
                 raise DzError(
-                    f"{LIB_PATH} is not built; run `python -m dizo_amd.build` "
+                    f"{path} is not built; run `python -m dizo_amd.build` "
                     "(or __graft_entry__.build()) first")
-            L = C.CDLL(LIB_PATH)
+            L = C.CDLL(path)
             for name, (res, args) in SIGNATURES.items():
                 fn = getattr(L, name)
                 fn.restype = res

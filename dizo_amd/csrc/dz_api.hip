@@ -178,16 +178,24 @@ int32_t check_range(uint64_t p, uint64_t bytes, const char* what, int32_t i) {
 
 }  // namespace
 
+// Tiles of one size over all of a table's tensors, in device memory.
+struct ChunkList {
+  uint32_t elems = 0;  // tile size (elements)
+  uint32_t n = 0;      // number of tiles
+  DzChunk* d = nullptr;
+};
+
 struct dz_table {
   int device = -1;
   int32_t dtype = 0;
   bool projection = false;
   int32_t n = 0;
-  uint32_t chunk_elems = 0;
+  uint32_t chunk_elems = 0;  // tile size of the primary list (d_chunks)
   uint32_t nchunks = 0;
   std::vector<uint64_t> ptrs, aux, zoff;
   std::vector<int64_t> numels;
-  std::vector<uint32_t> group_begin;  // n + 1 chunk indices
+  std::vector<uint32_t> group_begin;  // n + 1 chunk indices (primary list)
+  ChunkList extra;                    // ZO tables: a second tile size, when launches need one
   DzChunk* d_chunks = nullptr;
   uint32_t* d_group_begin = nullptr;
   double* d_partials = nullptr;
@@ -211,6 +219,7 @@ int32_t check_table(const dz_table* t) {
 
 void free_table(dz_table* t) {
   if (t->d_chunks) (void)hipFree(t->d_chunks);
+  if (t->extra.d) (void)hipFree(t->extra.d);
   if (t->d_group_begin) (void)hipFree(t->d_group_begin);
   if (t->d_partials) (void)hipFree(t->d_partials);
   if (t->d_counters) (void)hipFree(t->d_counters);
@@ -231,21 +240,59 @@ int32_t check_group_outputs(const dz_table* t, const double* d_sumsq, const floa
 // Persistent grid of an RMW launch: as many 1024-thread workgroups as fit on
 // the device at once given the LDS delta table (64 KB: two per CU; 128 KB:
 // one per CU), but no more than there are tiles.
-uint32_t rmw_grid(const dz_table* t, int mode) {
+uint32_t rmw_grid(const dz_table* t, int mode, uint32_t ntiles) {
   const uint32_t per_cu = dz::rmw_lds_table_bytes(t->dtype, mode) <= 65536 ? 2u : 1u;
   const uint32_t g = per_cu * (uint32_t)t->dev->cus;
-  return t->nchunks < g ? t->nchunks : g;
+  return ntiles < g ? ntiles : g;
 }
 
 int32_t rmw(dz_table* t, int mode, const dz::DzScalars& s, const dz::DzScalarPtrs& p, void* stream) {
   int32_t rc = check_table(t);
   if (rc) return rc;
   if (t->projection) return fail(DZ_ERR_INVALID, "perturb/update need a ZO table (created without anchors)");
-  if (t->nchunks == 0) return DZ_OK;
-  hipError_t e = dz::launch_rmw(t->dtype, mode, t->d_chunks, t->nchunks, rmw_grid(t, mode), t->dev->tab[t->dtype],
-                                s, p, t->d_counters, (hipStream_t)stream);
+  const uint32_t want = (uint32_t)dz::rmw_chunk_elems(t->dtype, mode);
+  const DzChunk* chunks = t->d_chunks;
+  uint32_t ntiles = t->nchunks;
+  if (want != t->chunk_elems) {
+    if (want != t->extra.elems) return fail(DZ_ERR_INVALID, "internal: no tile list for this launch");
+    chunks = t->extra.d;
+    ntiles = t->extra.n;
+  }
+  if (ntiles == 0) return DZ_OK;
+  hipError_t e = dz::launch_rmw(t->dtype, mode, chunks, ntiles, rmw_grid(t, mode, ntiles),
+                                t->dev->tab[t->dtype], s, p, t->d_counters, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "rmw kernel launch");
   return DZ_OK;
+}
+
+// Tiles of `elems` elements over every registered tensor, in tensor order.
+void build_chunks(const dz_table* t, uint32_t elems, std::vector<DzChunk>* out,
+                  std::vector<uint32_t>* group_begin) {
+  const int es = elem_size(t->dtype);
+  out->clear();
+  if (group_begin) group_begin->assign(1, 0u);
+  for (int32_t i = 0; i < t->n; ++i) {
+    const int64_t ne = t->numels[i];
+    const uint64_t p = t->ptrs[i], a = t->aux[i], z = t->zoff[i];
+    const bool aligned = (p % 16 == 0) && (a % 16 == 0);
+    for (int64_t s = 0; s < ne; s += elems) {
+      DzChunk c;
+      c.ptr = p + (uint64_t)s * es;
+      c.aux = t->projection ? a + (uint64_t)s * es : 0;
+      c.zgroup = (z + (uint64_t)s) >> 3;
+      c.n = (uint32_t)((ne - s) < (int64_t)elems ? (ne - s) : elems);
+      c.meta = (uint32_t)i | (aligned ? kDzMetaAligned : 0u);
+      out->push_back(c);
+    }
+    if (group_begin) group_begin->push_back((uint32_t)out->size());
+  }
+}
+
+hipError_t upload_chunks(const std::vector<DzChunk>& v, DzChunk** d) {
+  if (v.empty()) return hipSuccess;
+  hipError_t e = hipMalloc(d, v.size() * sizeof(DzChunk));
+  if (e == hipSuccess) e = hipMemcpy(*d, v.data(), v.size() * sizeof(DzChunk), hipMemcpyHostToDevice);
+  return e;
 }
 
 }  // namespace
@@ -298,11 +345,14 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
   t->projection = anchor_ptrs != nullptr;
   t->n = n;
   t->dev = ds;
-  t->chunk_elems = t->projection ? (uint32_t)dz::kProjChunk : (uint32_t)dz::rmw_chunk_elems(dtype);
+  // ZO tables: the primary tile list serves the pair-table launches
+  // (restore+update), the extra list the perturb/update launches when their
+  // tile size differs.
+  t->chunk_elems = t->projection ? (uint32_t)dz::kProjChunk
+                                 : (uint32_t)dz::rmw_chunk_elems(dtype, dz::kModeRestoreUpdate);
   const int es = elem_size(dtype);
-  std::vector<DzChunk> chunks;
   uint64_t z = 0;
-  t->group_begin.push_back(0);
+  uint64_t total_tiles = 0;
   for (int32_t i = 0; i < n; ++i) {
     const int64_t ne = numels[i];
     if (ne < 0) {
@@ -330,29 +380,27 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
     t->aux.push_back(a);
     t->numels.push_back(ne);
     t->zoff.push_back(z);
-    const bool aligned = (p % 16 == 0) && (a % 16 == 0);
-    for (int64_t s = 0; s < ne; s += t->chunk_elems) {
-      DzChunk c;
-      c.ptr = p + (uint64_t)s * es;
-      c.aux = t->projection ? a + (uint64_t)s * es : 0;
-      c.zgroup = (z + (uint64_t)s) >> 3;
-      c.n = (uint32_t)((ne - s) < (int64_t)t->chunk_elems ? (ne - s) : t->chunk_elems);
-      c.meta = (uint32_t)i | (aligned ? kDzMetaAligned : 0u);
-      chunks.push_back(c);
-      if (chunks.size() >= 0xffffffffull) {
-        free_table(t);
-        return fail(DZ_ERR_INVALID, "too many chunks");
-      }
-    }
-    t->group_begin.push_back((uint32_t)chunks.size());
+    // the smallest tile size bounds the tile count
+    total_tiles += ((uint64_t)ne + 8191u) / 8192u;
     z += ((uint64_t)ne + 7u) & ~(uint64_t)7u;
   }
+  if (total_tiles >= 0xffffffffull) {
+    free_table(t);
+    return fail(DZ_ERR_INVALID, "too many tiles");
+  }
+  std::vector<DzChunk> chunks;
+  build_chunks(t, t->chunk_elems, &chunks, &t->group_begin);
   t->nchunks = (uint32_t)chunks.size();
-  hipError_t e = hipSuccess;
-  if (t->nchunks > 0) {
-    e = hipMalloc(&t->d_chunks, chunks.size() * sizeof(DzChunk));
-    if (e == hipSuccess)
-      e = hipMemcpy(t->d_chunks, chunks.data(), chunks.size() * sizeof(DzChunk), hipMemcpyHostToDevice);
+  hipError_t e = upload_chunks(chunks, &t->d_chunks);
+  if (e == hipSuccess && !t->projection) {
+    const uint32_t narrow = (uint32_t)dz::rmw_chunk_elems(dtype, dz::kModePerturb);
+    if (narrow != t->chunk_elems) {
+      std::vector<DzChunk> fine;
+      build_chunks(t, narrow, &fine, nullptr);
+      t->extra.elems = narrow;
+      t->extra.n = (uint32_t)fine.size();
+      e = upload_chunks(fine, &t->extra.d);
+    }
   }
   if (e == hipSuccess && t->projection) {
     // The finalize kernel always runs, so these exist even with no chunks.
@@ -405,23 +453,31 @@ int32_t dz_table_z_offset(const dz_table* t, int32_t idx, uint64_t* out) {
 }
 
 int32_t dz_perturb(dz_table* t, uint64_t seed, float scale, float eps, const uint64_t* d_seed, void* stream) {
-  dz::DzScalars s{seed, scale, eps, 0.0f, 0.0f};
-  dz::DzScalarPtrs p{d_seed, nullptr, nullptr};
+  dz::DzScalars s{seed, 0, scale, eps, 0.0f, 0.0f};
+  dz::DzScalarPtrs p{d_seed, nullptr, nullptr, nullptr};
   return rmw(t, dz::kModePerturb, s, p, stream);
 }
 
 int32_t dz_update(dz_table* t, uint64_t seed, float grad, float lr, const uint64_t* d_seed, const void* d_grad,
                   const float* d_lr, void* stream) {
-  dz::DzScalars s{seed, 0.0f, 0.0f, grad, lr};
-  dz::DzScalarPtrs p{d_seed, d_grad, d_lr};
+  dz::DzScalars s{seed, 0, 0.0f, 0.0f, grad, lr};
+  dz::DzScalarPtrs p{d_seed, nullptr, d_grad, d_lr};
   return rmw(t, dz::kModeUpdate, s, p, stream);
 }
 
 int32_t dz_restore_update(dz_table* t, uint64_t seed, float eps, float grad, float lr, const uint64_t* d_seed,
                           const void* d_grad, const float* d_lr, void* stream) {
-  dz::DzScalars s{seed, 1.0f, eps, grad, lr};
-  dz::DzScalarPtrs p{d_seed, d_grad, d_lr};
+  dz::DzScalars s{seed, 0, 1.0f, eps, grad, lr};
+  dz::DzScalarPtrs p{d_seed, nullptr, d_grad, d_lr};
   return rmw(t, dz::kModeRestoreUpdate, s, p, stream);
+}
+
+int32_t dz_restore_update_perturb(dz_table* t, uint64_t seed, uint64_t next_seed, float eps, float grad, float lr,
+                                  const uint64_t* d_seed, const uint64_t* d_next_seed, const void* d_grad,
+                                  const float* d_lr, void* stream) {
+  dz::DzScalars s{seed, next_seed, 1.0f, eps, grad, lr};
+  dz::DzScalarPtrs p{d_seed, d_next_seed, d_grad, d_lr};
+  return rmw(t, dz::kModeRestoreUpdatePerturb, s, p, stream);
 }
 
 int32_t dz_normals(uint64_t seed, uint32_t stream_id, uint64_t offset, int64_t n, int32_t dtype, void* d_out,

@@ -75,9 +75,15 @@ DZ_HD DzU4 dz_philox4x32(DzU4 c, uint32_t k0, uint32_t k1) {
     dz_mulhilo32(0xD2511F53u, c.x, &lo0, &hi0);
     dz_mulhilo32(0xCD9E8D57u, c.z, &lo1, &hi1);
     DzU4 n;
+#if defined(__HIP_DEVICE_COMPILE__)
+    // gfx950 three-input bitwise op; truth table 0x96 is a ^ b ^ c
+    n.x = __builtin_amdgcn_bitop3_b32(hi1, c.y, k0, 0x96);
+    n.z = __builtin_amdgcn_bitop3_b32(hi0, c.w, k1, 0x96);
+#else
     n.x = hi1 ^ c.y ^ k0;
-    n.y = lo1;
     n.z = hi0 ^ c.w ^ k1;
+#endif
+    n.y = lo1;
     n.w = lo0;
     c = n;
     k0 += 0x9E3779B9u;

@@ -7,27 +7,51 @@
 
 namespace dz {
 
-enum RmwMode : int { kModePerturb = 0, kModeUpdate = 1, kModeRestoreUpdate = 2 };
+enum RmwMode : int {
+  kModePerturb = 0,               // theta + b(z)
+  kModeUpdate = 1,                // theta - d(z)
+  kModeRestoreUpdate = 2,         // theta + b(z) - d(z)
+  kModeRestoreUpdatePerturb = 3,  // theta + b(z) - d(z) + b(z'), z' from a second seed
+};
+// Modes whose table entries hold the pair (b, -d).
+__host__ __device__ constexpr bool rmw_pair_mode(int mode) {
+  return mode == kModeRestoreUpdate || mode == kModeRestoreUpdatePerturb;
+}
 enum ProjMode : int { kProjSumsq = 0, kProjApply = 1, kProjReverse = 2, kProjReverseSumsq = 3 };
 
 // Read-modify-write kernel geometry. A workgroup of 1024 threads takes one
 // tile (chunk) at a time from the table's work counters; each thread owns
-// kRmwGroups16 (16-bit T) or kRmwGroups32 (fp32) groups of 8 elements per
-// tile, i.e. 128 KB of theta per tile for every dtype.
+// rmw_groups(dtype, mode) groups of 8 elements per tile. Measured on the
+// MI355X at OPT-13B size: launches whose LDS table is 64 KB (two workgroups
+// per CU) stream best with 16 KB tiles (one group per thread, 6.1 TB/s);
+// launches with a 128 KB table (one workgroup per CU) with 64 KB tiles
+// (6.2 TB/s for restore+update). The macros let experiments build others.
+#ifndef DZ_RMW_GROUPS_NARROW
+#define DZ_RMW_GROUPS_NARROW 1
+#endif
+#ifndef DZ_RMW_GROUPS_WIDE16
+#define DZ_RMW_GROUPS_WIDE16 4
+#endif
+#ifndef DZ_RMW_GROUPS_WIDE32
+#define DZ_RMW_GROUPS_WIDE32 2
+#endif
+#ifndef DZ_RMW_COUNTERS
+#define DZ_RMW_COUNTERS 8
+#endif
 constexpr int kRmwThreads = 1024;
-constexpr int kRmwGroups16 = 8;
-constexpr int kRmwGroups32 = 4;
-constexpr int kRmwChunk16 = kRmwThreads * kRmwGroups16 * 8;  // 65536 elements
-constexpr int kRmwChunk32 = kRmwThreads * kRmwGroups32 * 8;  // 32768 elements
-__host__ __device__ constexpr int rmw_chunk_elems(int dtype) {
-  return dtype == DZ_F32 ? kRmwChunk32 : kRmwChunk16;
+__host__ __device__ constexpr int rmw_groups(int dtype, int mode) {
+  return dtype == DZ_F32 ? DZ_RMW_GROUPS_WIDE32 : (rmw_pair_mode(mode) ? DZ_RMW_GROUPS_WIDE16 : DZ_RMW_GROUPS_NARROW);
+}
+// Elements per tile of an RMW launch (the table's chunk size for that launch).
+__host__ __device__ constexpr int rmw_chunk_elems(int dtype, int mode) {
+  return kRmwThreads * rmw_groups(dtype, mode) * 8;
 }
 
 // LDS bytes of the per-launch delta table of an RMW launch: 16-bit entries
 // for perturb/update of 16-bit T, 32-bit entries otherwise (fp32 deltas, or
 // the (restore delta, update delta) pair of a fused restore+update).
 __host__ __device__ constexpr int rmw_lds_table_bytes(int dtype, int mode) {
-  return (dtype == DZ_F32 || mode == kModeRestoreUpdate) ? kDzTabEntries * 4 : kDzTabEntries * 2;
+  return (dtype == DZ_F32 || rmw_pair_mode(mode)) ? kDzTabEntries * 4 : kDzTabEntries * 2;
 }
 
 // Work counters of a table, one set per table: kCounters tile dispensers 128
@@ -35,7 +59,7 @@ __host__ __device__ constexpr int rmw_lds_table_bytes(int dtype, int mode) {
 // is created; the last workgroup of every RMW launch puts them back to zero,
 // so consecutive launches on one stream need no reset (and no memset in a
 // captured graph). Launches of one table must not overlap in time.
-constexpr int kCounters = 8;
+constexpr int kCounters = DZ_RMW_COUNTERS;
 constexpr int kCounterStride = 32;  // uint32 slots (128 bytes)
 constexpr int kCounterWords = (kCounters + 1) * kCounterStride;
 
@@ -47,6 +71,7 @@ constexpr int kProjChunk = 8192;
 // By-value scalars of one RMW launch.
 struct DzScalars {
   uint64_t seed;
+  uint64_t seed2;  // seed of the next step's perturbation (kModeRestoreUpdatePerturb)
   float scale;  // scaling_factor s of the perturbation
   float eps;    // zo_eps
   float grad;   // projected_grad g
@@ -56,7 +81,8 @@ struct DzScalars {
 // Optional device-resident overrides (read by the kernel when non-null), so a
 // captured graph can replay with a new seed / gradient / learning rate.
 struct DzScalarPtrs {
-  const uint64_t* seed;  // device uint64
+  const uint64_t* seed;   // device uint64
+  const uint64_t* seed2;  // device uint64
   const void* grad;      // device scalar of the table dtype T
   const float* lr;       // device fp32
 };

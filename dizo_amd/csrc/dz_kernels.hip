@@ -96,6 +96,7 @@ __device__ __forceinline__ float load_scalar_T(const void* p) {
 template <int DT>
 __device__ __forceinline__ DzScalars resolve_scalars(DzScalars s, const DzScalarPtrs& p) {
   if (p.seed) s.seed = *p.seed;
+  if (p.seed2) s.seed2 = *p.seed2;
   if (p.grad) s.grad = load_scalar_T<DT>(p.grad);
   if (p.lr) s.lr = *p.lr;
   return s;
@@ -134,10 +135,10 @@ __device__ __forceinline__ uint32_t z_bits(const typename DT_<DT>::S* tab, uint3
 // ---------------------------------------------------------------------------
 template <int DT, int MODE>
 struct RmwTraits {
-  static constexpr bool kWide = (DT == DZ_F32 || MODE == kModeRestoreUpdate);
+  static constexpr bool kWide = (DT == DZ_F32 || rmw_pair_mode(MODE));
   using E = typename std::conditional<kWide, uint32_t, uint16_t>::type;
-  static constexpr int kGroups = DT == DZ_F32 ? kRmwGroups32 : kRmwGroups16;
-  static constexpr int kChunk = kRmwThreads * kGroups * 8;
+  static constexpr int kGroups = rmw_groups(DT, MODE);
+  static constexpr int kChunk = rmw_chunk_elems(DT, MODE);
   // Waves per SIMD when the LDS table lets two workgroups share a CU (the
   // register budget then is 64 VGPRs), else one workgroup (4 waves).
   static constexpr int kWavesPerEU = kWide ? 4 : 8;
@@ -155,7 +156,7 @@ __device__ __forceinline__ uint32_t table_entry(uint32_t qbits, const DzScalars&
   } else if constexpr (MODE == kModeUpdate) {
     return DT_<DT>::from_f(d) ^ kSign;
   } else if constexpr (DT == DZ_F32) {
-    return qbits;
+    return qbits;  // restore+update(+perturb) in fp32: z itself
   } else {
     return DT_<DT>::from_f(b) | ((DT_<DT>::from_f(d) ^ kSign) << 16);
   }
@@ -188,10 +189,12 @@ __device__ __forceinline__ uint32_t add_one(uint32_t a, uint32_t b) {
   }
 }
 
-// Two 16-bit elements (packed in `th`) whose z fields are the halves of `w`.
+// Two 16-bit elements (packed in `th`) whose z fields are the halves of `w`
+// (and, for the step-fused mode, whose next-step z fields are the halves of w2).
 template <int DT, int MODE>
-__device__ __forceinline__ uint32_t apply_pair16(uint32_t th, uint32_t w, const typename RmwTraits<DT, MODE>::E* tab) {
-  if constexpr (MODE != kModeRestoreUpdate) {
+__device__ __forceinline__ uint32_t apply_pair16(uint32_t th, uint32_t w, uint32_t w2,
+                                                 const typename RmwTraits<DT, MODE>::E* tab) {
+  if constexpr (!rmw_pair_mode(MODE)) {
     const uint32_t lo = (uint32_t)tab[w & 0x7fffu] ^ (w & 0x8000u);
     const uint32_t hi = (uint32_t)tab[(w >> 16) & 0x7fffu] ^ ((w >> 16) & 0x8000u);
     return add_pair<DT>(th, lo | (hi << 16));
@@ -201,28 +204,44 @@ __device__ __forceinline__ uint32_t apply_pair16(uint32_t th, uint32_t w, const 
     const uint32_t e1 = tab[(w >> 16) & 0x7fffu] ^ (((w >> 16) & 0x8000u) * 0x10001u);
     const uint32_t b = (e0 & 0xffffu) | (e1 << 16);
     const uint32_t nd = (e0 >> 16) | (e1 & 0xffff0000u);
-    return add_pair<DT>(add_pair<DT>(th, b), nd);
+    uint32_t r = add_pair<DT>(add_pair<DT>(th, b), nd);
+    if constexpr (MODE == kModeRestoreUpdatePerturb) {
+      // the next step's +1 perturbation uses the same b (same scale and eps)
+      const uint32_t f0 = (tab[w2 & 0x7fffu] ^ (w2 & 0x8000u)) & 0xffffu;
+      const uint32_t f1 = (tab[(w2 >> 16) & 0x7fffu] ^ ((w2 >> 16) & 0x8000u)) & 0xffffu;
+      r = add_pair<DT>(r, f0 | (f1 << 16));
+    }
+    return r;
   }
 }
 
-// One element with 16-bit z field h.
+// One element with 16-bit z field h (and next-step field h2).
 template <int DT, int MODE>
-__device__ __forceinline__ uint32_t apply_one(uint32_t th, uint32_t h, const typename RmwTraits<DT, MODE>::E* tab,
-                                              const DzScalars& sc) {
+__device__ __forceinline__ uint32_t apply_one(uint32_t th, uint32_t h, uint32_t h2,
+                                              const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc) {
   if constexpr (DT == DZ_F32) {
     const uint32_t e = tab[h & 0x7fffu] ^ ((h & 0x8000u) << 16);
-    if constexpr (MODE != kModeRestoreUpdate) {
+    if constexpr (!rmw_pair_mode(MODE)) {
       return __float_as_uint(__uint_as_float(th) + __uint_as_float(e));
     } else {
       const float z = __uint_as_float(e);
       const float th1 = __uint_as_float(op_perturb<DZ_F32>(__uint_as_float(th), z, 1.0f, sc.eps));
-      return op_update<DZ_F32>(th1, z, sc.grad, sc.lr);
+      const uint32_t r = op_update<DZ_F32>(th1, z, sc.grad, sc.lr);
+      if constexpr (MODE == kModeRestoreUpdatePerturb) {
+        const float z2 = __uint_as_float(tab[h2 & 0x7fffu] ^ ((h2 & 0x8000u) << 16));
+        return op_perturb<DZ_F32>(__uint_as_float(r), z2, 1.0f, sc.eps);
+      }
+      return r;
     }
-  } else if constexpr (MODE != kModeRestoreUpdate) {
+  } else if constexpr (!rmw_pair_mode(MODE)) {
     return add_one<DT>(th, (uint32_t)tab[h & 0x7fffu] ^ (h & 0x8000u));
   } else {
     const uint32_t e = tab[h & 0x7fffu] ^ ((h & 0x8000u) * 0x10001u);
-    return add_one<DT>(add_one<DT>(th, e & 0xffffu), e >> 16);
+    uint32_t r = add_one<DT>(add_one<DT>(th, e & 0xffffu), e >> 16);
+    if constexpr (MODE == kModeRestoreUpdatePerturb) {
+      r = add_one<DT>(r, (tab[h2 & 0x7fffu] ^ (h2 & 0x8000u)) & 0xffffu);
+    }
+    return r;
   }
 }
 
@@ -266,6 +285,7 @@ __device__ __forceinline__ void rmw_chunk(const DzChunk& ch, const typename RmwT
   using Tr = RmwTraits<DT, MODE>;
   using S = typename DT_<DT>::S;
   constexpr int G = Tr::kGroups;
+  constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
   char* base = (char*)ch.ptr;
   if (ch.n == (uint32_t)Tr::kChunk && (ch.meta & kDzMetaAligned) != 0u) {
     if constexpr (DT != DZ_F32) {
@@ -276,11 +296,12 @@ __device__ __forceinline__ void rmw_chunk(const DzChunk& ch, const typename RmwT
       for (int u = 0; u < G; ++u) {
         const uint32_t g = threadIdx.x + u * kRmwThreads;
         const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
+        const DzU4 w2 = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, ch.zgroup + g) : w;
         dz_u32x4 o;
-        o.x = apply_pair16<DT, MODE>(v[u].x, w.x, tab);
-        o.y = apply_pair16<DT, MODE>(v[u].y, w.y, tab);
-        o.z = apply_pair16<DT, MODE>(v[u].z, w.z, tab);
-        o.w = apply_pair16<DT, MODE>(v[u].w, w.w, tab);
+        o.x = apply_pair16<DT, MODE>(v[u].x, w.x, w2.x, tab);
+        o.y = apply_pair16<DT, MODE>(v[u].y, w.y, w2.y, tab);
+        o.z = apply_pair16<DT, MODE>(v[u].z, w.z, w2.z, tab);
+        o.w = apply_pair16<DT, MODE>(v[u].w, w.w, w2.w, tab);
         st_stream(base + (size_t)g * 16, o);
       }
     } else {
@@ -295,15 +316,16 @@ __device__ __forceinline__ void rmw_chunk(const DzChunk& ch, const typename RmwT
       for (int u = 0; u < G; ++u) {
         const uint32_t g = threadIdx.x + u * kRmwThreads;
         const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
+        const DzU4 w2 = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, ch.zgroup + g) : w;
         dz_u32x4 o0, o1;
-        o0.x = apply_one<DT, MODE>(v[u][0].x, w.x & 0xffffu, tab, sc);
-        o0.y = apply_one<DT, MODE>(v[u][0].y, w.x >> 16, tab, sc);
-        o0.z = apply_one<DT, MODE>(v[u][0].z, w.y & 0xffffu, tab, sc);
-        o0.w = apply_one<DT, MODE>(v[u][0].w, w.y >> 16, tab, sc);
-        o1.x = apply_one<DT, MODE>(v[u][1].x, w.z & 0xffffu, tab, sc);
-        o1.y = apply_one<DT, MODE>(v[u][1].y, w.z >> 16, tab, sc);
-        o1.z = apply_one<DT, MODE>(v[u][1].z, w.w & 0xffffu, tab, sc);
-        o1.w = apply_one<DT, MODE>(v[u][1].w, w.w >> 16, tab, sc);
+        o0.x = apply_one<DT, MODE>(v[u][0].x, w.x & 0xffffu, w2.x & 0xffffu, tab, sc);
+        o0.y = apply_one<DT, MODE>(v[u][0].y, w.x >> 16, w2.x >> 16, tab, sc);
+        o0.z = apply_one<DT, MODE>(v[u][0].z, w.y & 0xffffu, w2.y & 0xffffu, tab, sc);
+        o0.w = apply_one<DT, MODE>(v[u][0].w, w.y >> 16, w2.y >> 16, tab, sc);
+        o1.x = apply_one<DT, MODE>(v[u][1].x, w.z & 0xffffu, w2.z & 0xffffu, tab, sc);
+        o1.y = apply_one<DT, MODE>(v[u][1].y, w.z >> 16, w2.z >> 16, tab, sc);
+        o1.z = apply_one<DT, MODE>(v[u][1].z, w.w & 0xffffu, w2.w & 0xffffu, tab, sc);
+        o1.w = apply_one<DT, MODE>(v[u][1].w, w.w >> 16, w2.w >> 16, tab, sc);
         st_stream(base + (size_t)g * 32, o0);
         st_stream(base + (size_t)g * 32 + 16, o1);
       }
@@ -312,11 +334,13 @@ __device__ __forceinline__ void rmw_chunk(const DzChunk& ch, const typename RmwT
     // Partial or misaligned tile: element by element, bounds-checked.
     for (uint32_t g = threadIdx.x; g * 8u < ch.n; g += kRmwThreads) {
       const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
+      const DzU4 w2 = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, ch.zgroup + g) : w;
       const uint32_t m = min(8u, ch.n - g * 8u);
       for (uint32_t j = 0; j < m; ++j) {
         const uint32_t h = (word_of(w, (int)(j >> 1)) >> (16 * (j & 1))) & 0xffffu;
+        const uint32_t h2 = (word_of(w2, (int)(j >> 1)) >> (16 * (j & 1))) & 0xffffu;
         S* p = (S*)(base + (size_t)(g * 8u + j) * sizeof(S));
-        *p = (S)apply_one<DT, MODE>((uint32_t)*p, h, tab, sc);
+        *p = (S)apply_one<DT, MODE>((uint32_t)*p, h, h2, tab, sc);
       }
     }
   }
@@ -594,6 +618,10 @@ static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunk
       break;
     case kModeRestoreUpdate:
       hipLaunchKernelGGL((rmw_kernel<DT, kModeRestoreUpdate>), dim3(grid), dim3(kRmwThreads), 0,
+                         st, chunks, nchunks, tab, s, p, counters);
+      break;
+    case kModeRestoreUpdatePerturb:
+      hipLaunchKernelGGL((rmw_kernel<DT, kModeRestoreUpdatePerturb>), dim3(grid), dim3(kRmwThreads), 0,
                          st, chunks, nchunks, tab, s, p, counters);
       break;
     default:

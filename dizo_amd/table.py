@@ -146,6 +146,13 @@ class ZOTable(_Table):
         L.call("dz_restore_update", self.handle, int(seed), float(eps), float(grad), float(lr),
                _ptr(d_seed), _ptr(d_grad), _ptr(d_lr), stream_handle(stream))
 
+    def restore_update_perturb(self, seed: int, next_seed: int, eps: float, grad: float, lr: float, *,
+                               d_seed=None, d_next_seed=None, d_grad=None, d_lr=None, stream=None) -> None:
+        """Restore + update of step `seed`, then the +1 perturbation of step `next_seed`, in one pass."""
+        self._check_scalar(d_grad, d_lr)
+        L.call("dz_restore_update_perturb", self.handle, int(seed), int(next_seed), float(eps), float(grad),
+               float(lr), _ptr(d_seed), _ptr(d_next_seed), _ptr(d_grad), _ptr(d_lr), stream_handle(stream))
+
     def _check_scalar(self, d_grad, d_lr):
         if d_grad is not None and (d_grad.dtype != self.dtype or d_grad.device != self.device):
             raise DzError(f"d_grad must be a {self.dtype} scalar on {self.device}")

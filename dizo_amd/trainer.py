@@ -25,9 +25,13 @@ What differs from the reference, by design:
     user code is detected and the tables are rebuilt;
   * the restore pass that ends ``zo_step`` is deferred and fused with the
     update pass of ``zo_update`` (one read-modify-write instead of two, with
-    the same per-element arithmetic). Any forward of the model, any
-    perturbation and ``zo_flush()`` apply a pending restore first, so the
-    parameters a caller can observe are the reference's;
+    the same per-element arithmetic); with ``zo_fuse_next_perturb`` that pass
+    is deferred again and fused with the first perturbation of the next
+    ``zo_step`` (two passes per step instead of three). Any forward of the
+    model, any other perturbation and ``zo_flush()`` apply pending work
+    first, so the parameters a caller can observe through the model are the
+    reference's (code that reads parameter storage directly between two steps
+    calls ``zo_flush()`` first);
   * ``torch.normal`` z (torch's Philox + Box-Muller) is replaced by the
     library's z: Philox4x32-10 keyed by the seed, 16 bits per element mapped
     through a 15-bit normal quantile table. Seeds, scaling factors, rounding
@@ -67,8 +71,11 @@ class ZOArguments:
     n_gpu: int = 1
     logging_nan_inf_filter: bool = True
     seed: int = 26
-    # build-specific: fuse the restore of zo_step with the update of zo_update
+    # build-specific pass fusion (same per-element arithmetic, fewer passes):
+    # the restore of zo_step with the update of zo_update, and that pass with
+    # the first perturbation of the next zo_step
     zo_fuse_restore: bool = True
+    zo_fuse_next_perturb: bool = True
 
 
 def layout_z_offsets(numels: Sequence[int]) -> List[int]:
@@ -220,7 +227,8 @@ class ZOTrainerMixin:
         self.zo_random_seed = None
         self.projected_grad = None
         self._zo_tabs = None
-        self._pending_restore = None
+        self._pending_restore = None  # (seed, eps): the +1 that ends zo_step
+        self._pending_update = None   # (seed, eps, g, lr): restore + update of zo_update
         self.kernel_timer = None
         self._hook = model.register_forward_pre_hook(lambda m, a: self.zo_flush())
 
@@ -247,7 +255,14 @@ class ZOTrainerMixin:
 
     # -------------------------------------------------------------- step --
     def zo_flush(self) -> None:
-        """Applies a deferred restore (the +1 perturbation that ends zo_step)."""
+        """Applies deferred work: a pending restore+update, or a pending restore
+        (the +1 perturbation that ends zo_step)."""
+        pu = self._pending_update
+        if pu is not None:
+            self._pending_update = None
+            seed, eps, g, lr = pu
+            tabs = self._zo_tables()
+            self._launch("restore_update", lambda t: t.restore_update(seed, eps, g, lr), tabs)
         pending = self._pending_restore
         if pending is not None:
             self._pending_restore = None
@@ -257,12 +272,22 @@ class ZOTrainerMixin:
 
     def zo_perturb_parameters(self, random_seed=None, scaling_factor=1):
         """trainer.py:1429-1444: theta <- theta + scaling_factor * z * zo_eps, in place."""
-        self.zo_flush()
         seed = random_seed if random_seed is not None else self.zo_random_seed
-        torch.manual_seed(seed)  # the reference re-seeds torch's generators here
-        tabs = self._zo_tables()
         eps = float(self.args.zo_eps)
         s = float(scaling_factor)
+        pu = self._pending_update
+        if pu is not None and s == 1.0 and pu[1] == eps and self._pending_restore is None:
+            # previous step's restore + update, then this +1, in one pass
+            self._pending_update = None
+            torch.manual_seed(seed)
+            tabs = self._zo_tables()
+            prev, _, g, lr = pu
+            self._launch("restore_update_perturb",
+                         lambda t: t.restore_update_perturb(prev, seed, eps, g, lr), tabs)
+            return
+        self.zo_flush()
+        torch.manual_seed(seed)  # the reference re-seeds torch's generators here
+        tabs = self._zo_tables()
         self._launch("perturb", lambda t: t.perturb(seed, s, eps), tabs)
 
     def _prepare_inputs(self, inputs):
@@ -304,15 +329,19 @@ class ZOTrainerMixin:
         torch.manual_seed(seed)
         tabs = self._zo_tables()
         g, lr = float(self.projected_grad), float(self._get_learning_rate())
+        event_due = (self.state.global_step + 1) % DIZO_INTERVAL == 0 and args.enhanced
         pending = self._pending_restore
         if pending is not None and pending[0] == seed:
             self._pending_restore = None
             eps = pending[1]
-            self._launch("restore_update", lambda t: t.restore_update(seed, eps, g, lr), tabs)
+            if getattr(args, "zo_fuse_next_perturb", False) and not event_due:
+                self._pending_update = (seed, eps, g, lr)  # applied with the next +1 perturbation
+            else:
+                self._launch("restore_update", lambda t: t.restore_update(seed, eps, g, lr), tabs)
         else:
             self.zo_flush()
             self._launch("update", lambda t: t.update(seed, g, lr), tabs)
-        if (self.state.global_step + 1) % DIZO_INTERVAL == 0 and args.enhanced:
+        if event_due:
             self.dizo_trainer.gamma_seed = seed
             if args.enhanced == "zo":
                 self.dizo_trainer.dizo_zo_iters(model, base_model=self.base_model)

@@ -105,6 +105,15 @@ int32_t dz_restore_update(dz_table* t, uint64_t seed, float eps, float grad, flo
                           const uint64_t* d_seed, const void* d_grad, const float* d_lr,
                           void* stream);
 
+/* The fused restore+update of step k (as dz_restore_update, z from `seed`)
+ * followed by the first perturbation (+1, same eps) of step k+1 (z from
+ * `next_seed`), in one pass: trainer.py:1593 and 1603-1608 of step k, then
+ * trainer.py:1580 of the next zo_step. Per element the three operations are
+ * applied in that order with the reference's rounding. */
+int32_t dz_restore_update_perturb(dz_table* t, uint64_t seed, uint64_t next_seed, float eps, float grad,
+                                  float lr, const uint64_t* d_seed, const uint64_t* d_next_seed,
+                                  const void* d_grad, const float* d_lr, void* stream);
+
 /* ---- z export / RNG (test and tooling use) ------------------------------ */
 
 /* n normals z(seed, stream_id, offset + i) in `dtype`, written densely to d_out.

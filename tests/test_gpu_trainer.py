@@ -52,12 +52,13 @@ def _setup(dt, seed=3):
 
 
 @pytest.mark.parametrize("dt", DTS)
-@pytest.mark.parametrize("fuse", [True, False])
+@pytest.mark.parametrize("fuse", ["none", "restore", "next"])
 def test_zo_steps_match_reference(dt, fuse):
     from dizo_amd.trainer import ZOArguments, ZOTrainer, select_trainable
     model_a, model_b, batches = _setup(dt)
     steps, lr0, eps = 5, 1e-3, 1e-3
-    args = ZOArguments(learning_rate=lr0, zo_eps=eps, max_steps=steps, enhanced=None, zo_fuse_restore=fuse)
+    args = ZOArguments(learning_rate=lr0, zo_eps=eps, max_steps=steps, enhanced=None,
+                       zo_fuse_restore=fuse != "none", zo_fuse_next_perturb=fuse == "next")
     np.random.seed(26)
     tr = ZOTrainer(model_a, args)
     losses_a = [tr.training_step(batches[k]) for k in range(steps)]

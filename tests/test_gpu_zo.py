@@ -128,6 +128,29 @@ def test_full_step_sequence_matches_oracle(dt):
 
 
 @pytest.mark.parametrize("dt", DTS)
+def test_restore_update_perturb_matches_oracle(dt):
+    """Restore + update of step seed, then +1 of step next_seed, in one pass: the
+    same bits as the three passes, and as the oracle."""
+    from dizo_amd.table import ZOTable
+    tensors, host, keep = _make_tensors(dt, 61)
+    clones = [t.clone() for t in tensors]
+    tab = ZOTable(tensors)
+    seed, nxt, eps, g, lr = 9090, 9091, 1e-3, 0.6875, 9.9e-07
+    tab.restore_update_perturb(seed, nxt, eps, g, lr)
+    z1, z2 = _z_host(tab, seed, dt), _z_host(tab, nxt, dt)
+    for i, (t, h) in enumerate(zip(tensors, host)):
+        want = A.perturb(A.restore_update(h, z1[i], eps, g, lr, dt), z2[i], 1, eps, dt)
+        assert_bits_equal(to_bits(t).ravel(), want, dt, f"fused3 tensor {i}")
+    tab2 = ZOTable(clones)
+    tab2.restore_update(seed, eps, g, lr)
+    tab2.perturb(nxt, 1.0, eps)
+    for i, (t, c) in enumerate(zip(tensors, clones)):
+        assert_bits_equal(to_bits(t).ravel(), to_bits(c).ravel(), dt, f"fused3 vs two passes, tensor {i}")
+    tab.close()
+    tab2.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
 def test_device_scalar_overrides(dt):
     """Seed / grad / lr read from device memory give the by-value results."""
     from dizo_amd.table import ZOTable
@@ -204,6 +227,12 @@ def test_multi_tile_launches_match_torch(dt, target):
     R.zo_update(ref, zs, g, lr)
     tab.update(seed, g, lr)
     R.zo_update(ref, zs, g, lr)
+    seed2 = seed + 1
+    zs2 = [tab.export_z(seed2, i) for i in range(len(tensors))]
+    tab.restore_update_perturb(seed, seed2, eps, g, lr)
+    R.zo_perturb_parameters(ref, zs, 1, eps)
+    R.zo_update(ref, zs, g, lr)
+    R.zo_perturb_parameters(ref, zs2, 1, eps)
     torch.cuda.synchronize()
     bad = [i for i, (t, r) in enumerate(zip(tensors, ref)) if not torch.equal(t.view(torch.int16 if dt != F32 else torch.int32),
                                                                            r.view(torch.int16 if dt != F32 else torch.int32))]
