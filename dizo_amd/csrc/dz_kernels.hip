@@ -142,6 +142,10 @@ struct RmwTraits {
   // Waves per SIMD when the LDS table lets two workgroups share a CU (the
   // register budget then is 64 VGPRs), else one workgroup (4 waves).
   static constexpr int kWavesPerEU = kWide ? 4 : 8;
+  // Load tile k+1 while tile k computes: pays off for the two-seed pass, whose
+  // ALU time (two Philox chains per group) is the largest; measured neutral to
+  // negative for the others.
+  static constexpr bool kPrefetch = MODE == kModeRestoreUpdatePerturb;
 };
 
 // Table entry for z = +Q_T[i] (qbits = bits of Q_T[i]).
@@ -278,70 +282,99 @@ __device__ __forceinline__ DzChunk uniform_chunk(const DzChunk& c) {
   return u;
 }
 
-// One tile of an RMW launch.
+// Registers of one full tile: kVecs 16-byte vectors per thread.
 template <int DT, int MODE>
-__device__ __forceinline__ void rmw_chunk(const DzChunk& ch, const typename RmwTraits<DT, MODE>::E* tab,
-                                          const DzScalars& sc) {
-  using Tr = RmwTraits<DT, MODE>;
-  using S = typename DT_<DT>::S;
-  constexpr int G = Tr::kGroups;
+struct TileRegs {
+  static constexpr int kVecs = (DT == DZ_F32 ? 2 : 1) * RmwTraits<DT, MODE>::kGroups;
+  dz_u32x4 v[kVecs];
+};
+
+template <int DT, int MODE>
+__device__ __forceinline__ bool full_tile(const DzChunk& ch) {
+  return ch.n == (uint32_t)RmwTraits<DT, MODE>::kChunk && (ch.meta & kDzMetaAligned) != 0u;
+}
+
+// Byte offset of vector i of this thread in a full tile: group u = i (16-bit)
+// or i / 2 (fp32, two vectors per group of 8 elements); groups are strided
+// by the workgroup so each load instruction covers contiguous memory.
+template <int DT>
+__device__ __forceinline__ size_t tile_vec_offset(int i) {
+  if constexpr (DT != DZ_F32) {
+    return (size_t)(threadIdx.x + i * kRmwThreads) * 16;
+  } else {
+    return (size_t)(threadIdx.x + (i >> 1) * kRmwThreads) * 32 + (size_t)(i & 1) * 16;
+  }
+}
+
+template <int DT, int MODE>
+__device__ __forceinline__ void load_tile(const DzChunk& ch, TileRegs<DT, MODE>& r) {
+  const char* base = (const char*)ch.ptr;
+#pragma unroll
+  for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_stream(base + tile_vec_offset<DT>(i));
+}
+
+// Applies the launch's operation to a full tile already in registers and stores it.
+template <int DT, int MODE>
+__device__ __forceinline__ void compute_store_tile(const DzChunk& ch, const TileRegs<DT, MODE>& r,
+                                                   const typename RmwTraits<DT, MODE>::E* tab,
+                                                   const DzScalars& sc) {
+  constexpr int G = RmwTraits<DT, MODE>::kGroups;
   constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
   char* base = (char*)ch.ptr;
-  if (ch.n == (uint32_t)Tr::kChunk && (ch.meta & kDzMetaAligned) != 0u) {
-    if constexpr (DT != DZ_F32) {
-      dz_u32x4 v[G];
+  // All Philox blocks of the tile first: G (or 2G) independent 10-round
+  // chains the scheduler can interleave.
+  DzU4 w[G], w2[G];
 #pragma unroll
-      for (int u = 0; u < G; ++u) v[u] = ld_stream(base + (size_t)(threadIdx.x + u * kRmwThreads) * 16);
+  for (int u = 0; u < G; ++u) {
+    const uint64_t q = ch.zgroup + threadIdx.x + u * kRmwThreads;
+    w[u] = dz_philox_group(sc.seed, kDzStreamParam, q);
+    w2[u] = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, q) : w[u];
+  }
+  if constexpr (DT != DZ_F32) {
 #pragma unroll
-      for (int u = 0; u < G; ++u) {
-        const uint32_t g = threadIdx.x + u * kRmwThreads;
-        const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
-        const DzU4 w2 = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, ch.zgroup + g) : w;
-        dz_u32x4 o;
-        o.x = apply_pair16<DT, MODE>(v[u].x, w.x, w2.x, tab);
-        o.y = apply_pair16<DT, MODE>(v[u].y, w.y, w2.y, tab);
-        o.z = apply_pair16<DT, MODE>(v[u].z, w.z, w2.z, tab);
-        o.w = apply_pair16<DT, MODE>(v[u].w, w.w, w2.w, tab);
-        st_stream(base + (size_t)g * 16, o);
-      }
-    } else {
-      dz_u32x4 v[G][2];
-#pragma unroll
-      for (int u = 0; u < G; ++u) {
-        const size_t off = (size_t)(threadIdx.x + u * kRmwThreads) * 32;
-        v[u][0] = ld_stream(base + off);
-        v[u][1] = ld_stream(base + off + 16);
-      }
-#pragma unroll
-      for (int u = 0; u < G; ++u) {
-        const uint32_t g = threadIdx.x + u * kRmwThreads;
-        const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
-        const DzU4 w2 = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, ch.zgroup + g) : w;
-        dz_u32x4 o0, o1;
-        o0.x = apply_one<DT, MODE>(v[u][0].x, w.x & 0xffffu, w2.x & 0xffffu, tab, sc);
-        o0.y = apply_one<DT, MODE>(v[u][0].y, w.x >> 16, w2.x >> 16, tab, sc);
-        o0.z = apply_one<DT, MODE>(v[u][0].z, w.y & 0xffffu, w2.y & 0xffffu, tab, sc);
-        o0.w = apply_one<DT, MODE>(v[u][0].w, w.y >> 16, w2.y >> 16, tab, sc);
-        o1.x = apply_one<DT, MODE>(v[u][1].x, w.z & 0xffffu, w2.z & 0xffffu, tab, sc);
-        o1.y = apply_one<DT, MODE>(v[u][1].y, w.z >> 16, w2.z >> 16, tab, sc);
-        o1.z = apply_one<DT, MODE>(v[u][1].z, w.w & 0xffffu, w2.w & 0xffffu, tab, sc);
-        o1.w = apply_one<DT, MODE>(v[u][1].w, w.w >> 16, w2.w >> 16, tab, sc);
-        st_stream(base + (size_t)g * 32, o0);
-        st_stream(base + (size_t)g * 32 + 16, o1);
-      }
+    for (int u = 0; u < G; ++u) {
+      dz_u32x4 o;
+      o.x = apply_pair16<DT, MODE>(r.v[u].x, w[u].x, w2[u].x, tab);
+      o.y = apply_pair16<DT, MODE>(r.v[u].y, w[u].y, w2[u].y, tab);
+      o.z = apply_pair16<DT, MODE>(r.v[u].z, w[u].z, w2[u].z, tab);
+      o.w = apply_pair16<DT, MODE>(r.v[u].w, w[u].w, w2[u].w, tab);
+      st_stream(base + tile_vec_offset<DT>(u), o);
     }
   } else {
-    // Partial or misaligned tile: element by element, bounds-checked.
-    for (uint32_t g = threadIdx.x; g * 8u < ch.n; g += kRmwThreads) {
-      const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
-      const DzU4 w2 = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, ch.zgroup + g) : w;
-      const uint32_t m = min(8u, ch.n - g * 8u);
-      for (uint32_t j = 0; j < m; ++j) {
-        const uint32_t h = (word_of(w, (int)(j >> 1)) >> (16 * (j & 1))) & 0xffffu;
-        const uint32_t h2 = (word_of(w2, (int)(j >> 1)) >> (16 * (j & 1))) & 0xffffu;
-        S* p = (S*)(base + (size_t)(g * 8u + j) * sizeof(S));
-        *p = (S)apply_one<DT, MODE>((uint32_t)*p, h, h2, tab, sc);
-      }
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const dz_u32x4 a = r.v[2 * u], b = r.v[2 * u + 1];
+      dz_u32x4 o0, o1;
+      o0.x = apply_one<DT, MODE>(a.x, w[u].x & 0xffffu, w2[u].x & 0xffffu, tab, sc);
+      o0.y = apply_one<DT, MODE>(a.y, w[u].x >> 16, w2[u].x >> 16, tab, sc);
+      o0.z = apply_one<DT, MODE>(a.z, w[u].y & 0xffffu, w2[u].y & 0xffffu, tab, sc);
+      o0.w = apply_one<DT, MODE>(a.w, w[u].y >> 16, w2[u].y >> 16, tab, sc);
+      o1.x = apply_one<DT, MODE>(b.x, w[u].z & 0xffffu, w2[u].z & 0xffffu, tab, sc);
+      o1.y = apply_one<DT, MODE>(b.y, w[u].z >> 16, w2[u].z >> 16, tab, sc);
+      o1.z = apply_one<DT, MODE>(b.z, w[u].w & 0xffffu, w2[u].w & 0xffffu, tab, sc);
+      o1.w = apply_one<DT, MODE>(b.w, w[u].w >> 16, w2[u].w >> 16, tab, sc);
+      st_stream(base + tile_vec_offset<DT>(2 * u), o0);
+      st_stream(base + tile_vec_offset<DT>(2 * u + 1), o1);
+    }
+  }
+}
+
+// Partial or misaligned tile: element by element, bounds-checked.
+template <int DT, int MODE>
+__device__ __forceinline__ void rmw_partial(const DzChunk& ch, const typename RmwTraits<DT, MODE>::E* tab,
+                                            const DzScalars& sc) {
+  using S = typename DT_<DT>::S;
+  constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
+  char* base = (char*)ch.ptr;
+  for (uint32_t g = threadIdx.x; g * 8u < ch.n; g += kRmwThreads) {
+    const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
+    const DzU4 w2 = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, ch.zgroup + g) : w;
+    const uint32_t m = min(8u, ch.n - g * 8u);
+    for (uint32_t j = 0; j < m; ++j) {
+      const uint32_t h = (word_of(w, (int)(j >> 1)) >> (16 * (j & 1))) & 0xffffu;
+      const uint32_t h2 = (word_of(w2, (int)(j >> 1)) >> (16 * (j & 1))) & 0xffffu;
+      S* p = (S*)(base + (size_t)(g * 8u + j) * sizeof(S));
+      *p = (S)apply_one<DT, MODE>((uint32_t)*p, h, h2, tab, sc);
     }
   }
 }
@@ -368,8 +401,9 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
   using E = typename Tr::E;
   using S = typename DT_<DT>::S;
   __shared__ __attribute__((aligned(16))) E tab[kDzTabEntries];
-  __shared__ uint32_t sidx[3];    // tile indices k, k+1, k+2 (>= nchunks: none)
-  __shared__ DzChunk sdesc[2];    // descriptors of tiles k, k+1
+  // Tile bookkeeping rings: indices of tiles k .. k+3, descriptors of k .. k+2.
+  __shared__ uint32_t sidx[4];
+  __shared__ DzChunk sdesc[3];
   const DzScalars sc = resolve_scalars<DT>(sc_in, sp);
   {
     const S* q = (const S*)qtab;
@@ -382,45 +416,74 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
   const uint32_t j = rfl_u32((blockIdx.x >> 3) % ncnt);
   uint32_t* mine = counters + j * kCounterStride;
   const uint64_t nch = nchunks;
-  // Two-deep pipeline kept by thread 0: while tile k streams, the index of
-  // tile k+2 is taken from the counter and the descriptor of tile k+1 is
-  // loaded, so neither latency sits between two tiles.
+  // Pipeline kept by wave 0: while tile k streams, the index of tile k+3 is
+  // taken from the counter and the descriptor of tile k+2 is loaded, so
+  // neither latency sits between two tiles. The two-seed pass (Tr::kPrefetch)
+  // also loads tile k+1's data before computing tile k.
   if (threadIdx.x == 0) {
-    const uint64_t c0 = (uint64_t)atomicAdd(mine, 1u) * ncnt + j;
-    const uint64_t c1 = (uint64_t)atomicAdd(mine, 1u) * ncnt + j;
-    sidx[0] = (uint32_t)min(c0, nch);
-    sidx[1] = (uint32_t)min(c1, nch);
-    if (c0 < nch) sdesc[0] = chunks[c0];
+    uint64_t c[3];
+    for (int i = 0; i < 3; ++i) {
+      c[i] = (uint64_t)atomicAdd(mine, 1u) * ncnt + j;
+      sidx[i] = (uint32_t)min(c[i], nch);
+    }
+    if (c[0] < nch) sdesc[0] = chunks[c[0]];
+    if (c[1] < nch) sdesc[1] = chunks[c[1]];
   }
   __syncthreads();
+  TileRegs<DT, MODE> cur, nxt;
+  bool have_cur = false;
+  if constexpr (Tr::kPrefetch) {
+    if (sidx[0] < nchunks) {
+      const DzChunk c0 = uniform_chunk(sdesc[0]);
+      if (full_tile<DT, MODE>(c0)) {
+        load_tile<DT, MODE>(c0, cur);
+        have_cur = true;
+      }
+    }
+  }
   for (uint32_t k = 0;; ++k) {
-    const uint32_t c = sidx[k % 3];
+    const uint32_t c = sidx[k % 4];
     if (c >= nchunks) break;
-    const DzChunk ch = uniform_chunk(sdesc[k & 1]);
-    // Wave 0 fetches the next descriptor with scalar loads (it is uniform,
-    // so it costs no vector registers); lane 0 takes the next index with a
-    // vector atomic. The anchor field is unused by ZO tables.
+    const DzChunk ch = uniform_chunk(sdesc[k % 3]);
+    // Wave 0 fetches a descriptor with scalar loads (it is uniform, so it
+    // costs no vector registers); lane 0 takes an index with a vector
+    // atomic. The anchor field is unused by ZO tables.
     uint32_t grabbed = 0;
     uint64_t n_ptr = 0, n_zg = 0;
     uint32_t n_n = 0, n_meta = 0;
-    bool have_next = false;
+    bool have_desc = false;
     if ((rfl_u32(threadIdx.x) >> 6) == 0) {  // wave 0 (uniform branch)
       if (threadIdx.x == 0) grabbed = atomicAdd(mine, 1u);
-      const uint32_t cn = rfl_u32(sidx[(k + 1) % 3]);
-      if (cn < nchunks) {
-        const DzChunk* src = chunks + cn;
+      const uint32_t cd = rfl_u32(sidx[(k + 2) % 4]);
+      if (cd < nchunks) {
+        const DzChunk* src = chunks + cd;
         n_ptr = src->ptr;
         n_zg = src->zgroup;
         n_n = src->n;
         n_meta = src->meta;
-        have_next = true;
+        have_desc = true;
       }
     }
-    rmw_chunk<DT, MODE>(ch, tab, sc);
+    bool have_next = false;
+    if constexpr (Tr::kPrefetch) {
+      if (sidx[(k + 1) % 4] < nchunks) {
+        const DzChunk cn = uniform_chunk(sdesc[(k + 1) % 3]);
+        if (full_tile<DT, MODE>(cn)) {
+          load_tile<DT, MODE>(cn, nxt);
+          have_next = true;
+        }
+      }
+    }
+    if (full_tile<DT, MODE>(ch)) {
+      if (!have_cur) load_tile<DT, MODE>(ch, cur);
+      compute_store_tile<DT, MODE>(ch, cur, tab, sc);
+    } else {
+      rmw_partial<DT, MODE>(ch, tab, sc);
+    }
     if (threadIdx.x == 0) {
-      sidx[(k + 2) % 3] = (uint32_t)min((uint64_t)grabbed * ncnt + j, nch);
-      if (have_next) {
-        DzChunk& d = sdesc[(k + 1) & 1];
+      sidx[(k + 3) % 4] = (uint32_t)min((uint64_t)grabbed * ncnt + j, nch);
+      if (have_desc) {
+        DzChunk& d = sdesc[(k + 2) % 3];
         d.ptr = n_ptr;
         d.aux = 0;
         d.zgroup = n_zg;
@@ -429,6 +492,10 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
       }
     }
     __syncthreads();
+    if constexpr (Tr::kPrefetch) {
+      cur = nxt;
+      have_cur = have_next;
+    }
   }
   if (threadIdx.x == 0) {
     const uint32_t done = atomicAdd(counters + kCounters * kCounterStride, 1u);
