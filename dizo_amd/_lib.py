@@ -19,6 +19,7 @@ DZ_PROJ_SUMSQ = 0
 DZ_PROJ_APPLY = 1
 DZ_PROJ_REVERSE = 2
 DZ_PROJ_REVERSE_SUMSQ = 3
+DZ_PROJ_APPLY_F32ALPHA = 4
 
 DZ_STREAM_PARAM = 0
 DZ_STREAM_GAMMA = 1
@@ -57,6 +58,7 @@ SIGNATURES = {
     "dz_philox": (_i32, [_u64, _u32, _u64, _i64, _p, _p]),
     "dz_group_sumsq": (_i32, [_p, _p, _p, _p, _p]),
     "dz_project": (_i32, [_p, _p, _i32, _p, _p, _p, _p]),
+    "dz_group_dot": (_i32, [_p, _p, _p, _p, _p]),
 }
 
 _lock = threading.Lock()

@@ -279,7 +279,7 @@ void build_chunks(const dz_table* t, uint32_t elems, std::vector<DzChunk>* out,
       DzChunk c;
       c.ptr = p + (uint64_t)s * es;
       c.aux = t->projection ? a + (uint64_t)s * es : 0;
-      c.zgroup = (z + (uint64_t)s) >> 3;
+      c.zgroup = t->projection ? (uint64_t)s : (z + (uint64_t)s) >> 3;
       c.n = (uint32_t)((ne - s) < (int64_t)elems ? (ne - s) : elems);
       c.meta = (uint32_t)i | (aligned ? kDzMetaAligned : 0u);
       out->push_back(c);
@@ -531,7 +531,7 @@ int32_t dz_group_sumsq(dz_table* t, double* d_sumsq, float* d_norm_f32, void* d_
     if (e != hipSuccess) return hip_fail(e, "sumsq kernel launch");
   }
   e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_sumsq, d_norm_f32,
-                          d_norm_T, (hipStream_t)stream);
+                          d_norm_T, true, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
   return DZ_OK;
 }
@@ -541,9 +541,11 @@ int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sum
   int32_t rc = check_table(t);
   if (rc) return rc;
   if (!t->projection) return fail(DZ_ERR_INVALID, "project needs a projection table");
-  if (mode != DZ_PROJ_APPLY && mode != DZ_PROJ_REVERSE && mode != DZ_PROJ_REVERSE_SUMSQ)
-    return fail(DZ_ERR_INVALID, "mode must be APPLY, REVERSE or REVERSE_SUMSQ");
-  rc = check_range((uint64_t)(uintptr_t)d_alpha, (uint64_t)t->n * elem_size(t->dtype), "alpha", 0);
+  if (mode != DZ_PROJ_APPLY && mode != DZ_PROJ_REVERSE && mode != DZ_PROJ_REVERSE_SUMSQ &&
+      mode != DZ_PROJ_APPLY_F32ALPHA)
+    return fail(DZ_ERR_INVALID, "mode must be APPLY, REVERSE, REVERSE_SUMSQ or APPLY_F32ALPHA");
+  const int alpha_size = mode == DZ_PROJ_APPLY_F32ALPHA ? 4 : elem_size(t->dtype);
+  rc = check_range((uint64_t)(uintptr_t)d_alpha, (uint64_t)t->n * alpha_size, "alpha", 0);
   if (!rc) rc = check_group_outputs(t, d_sumsq, d_norm_f32, d_norm_T);
   if (rc) return rc;
   if (t->nchunks > 0) {
@@ -553,9 +555,37 @@ int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sum
   }
   if (mode == DZ_PROJ_REVERSE_SUMSQ) {
     hipError_t e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_sumsq,
-                                       d_norm_f32, d_norm_T, (hipStream_t)stream);
+                                       d_norm_f32, d_norm_T, true, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
   }
+  return DZ_OK;
+}
+
+int32_t dz_group_dot(dz_table* t, const uint64_t* other_ptrs, double* d_dot, float* d_dot_f32, void* stream) {
+  int32_t rc = check_table(t);
+  if (rc) return rc;
+  if (!t->projection) return fail(DZ_ERR_INVALID, "group_dot needs a projection table");
+  if (!other_ptrs) return fail(DZ_ERR_INVALID, "other_ptrs is NULL");
+  if (t->n > dz::kMaxDotGroups)
+    return fail(DZ_ERR_INVALID, "group_dot takes at most " + std::to_string(dz::kMaxDotGroups) + " groups");
+  dz::DzPtrArray other{};
+  for (int32_t i = 0; i < t->n; ++i) {
+    if (t->numels[i] > 0) {
+      rc = check_range(other_ptrs[i], (uint64_t)t->numels[i] * elem_size(t->dtype), "other", i);
+      if (rc) return rc;
+    }
+    other.p[i] = other_ptrs[i];
+  }
+  rc = check_group_outputs(t, d_dot, d_dot_f32, nullptr);
+  if (rc) return rc;
+  hipError_t e = hipSuccess;
+  if (t->nchunks > 0) {
+    e = dz::launch_dot(t->dtype, t->d_chunks, t->nchunks, other, t->d_partials, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dot kernel launch");
+  }
+  e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_dot, d_dot_f32, nullptr,
+                          false, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
   return DZ_OK;
 }
 

@@ -45,7 +45,8 @@ constexpr int kDzTabEntries = 32768;  // quantile table entries (15-bit index)
 struct DzChunk {
   uint64_t ptr;     // byte address of the chunk's first element (theta)
   uint64_t aux;     // byte address of the matching anchor element (theta0), or 0
-  uint64_t zgroup;  // Philox counter q of the chunk's first element (e / 8)
+  uint64_t zgroup;  // ZO tables: Philox counter q of the chunk's first element (e / 8);
+                    // projection tables: element offset of the chunk in its tensor
   uint32_t n;       // number of elements in the chunk
   uint32_t meta;    // bits 0..23: tensor/group index; bit 31: all pointers 16-byte aligned
 };

@@ -17,7 +17,18 @@ enum RmwMode : int {
 __host__ __device__ constexpr bool rmw_pair_mode(int mode) {
   return mode == kModeRestoreUpdate || mode == kModeRestoreUpdatePerturb;
 }
-enum ProjMode : int { kProjSumsq = 0, kProjApply = 1, kProjReverse = 2, kProjReverseSumsq = 3 };
+enum ProjMode : int {
+  kProjSumsq = 0,         // per-chunk sums of R_T(theta - theta0)^2
+  kProjApply = 1,         // theta <- R(R(R(theta - theta0) * alpha) + theta0), alpha in T
+  kProjReverse = 2,       // theta <- R(R(R(theta - theta0) / alpha) + theta0)
+  kProjReverseSumsq = 3,  // REVERSE, then the sums of the new theta
+  kProjApplyF32 = 4,      // theta <- R_T(fp32(R(theta - theta0)) * alpha + theta0), alpha fp32
+};
+// Most groups a dot launch takes (their pointers travel as kernel arguments).
+constexpr int kMaxDotGroups = 128;
+struct DzPtrArray {
+  uint64_t p[kMaxDotGroups];
+};
 
 // Read-modify-write kernel geometry. A workgroup of 1024 threads takes one
 // tile (chunk) at a time from the table's work counters; each thread owns
@@ -92,8 +103,11 @@ hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchun
                       hipStream_t st);
 hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, const void* alpha,
                        double* partials, hipStream_t st);
+hipError_t launch_dot(int dtype, const DzChunk* chunks, uint32_t nchunks, const DzPtrArray& other,
+                      double* partials, hipStream_t st);
+// take_sqrt: norms (sqrt of the sums) or plain sums in the fp32 / T outputs.
 hipError_t launch_finalize(int dtype, const double* partials, const uint32_t* gbegin, uint32_t ngroups,
-                           double* sumsq, float* norm_f32, void* norm_T, hipStream_t st);
+                           double* sumsq, float* norm_f32, void* norm_T, bool take_sqrt, hipStream_t st);
 hipError_t launch_normals(int dtype, const void* tab, uint64_t seed, uint32_t stream, uint64_t offset,
                           uint64_t n, void* out, hipStream_t st);
 hipError_t launch_philox(uint64_t seed, uint32_t stream, uint64_t q0, uint64_t n, uint32_t* out,

@@ -511,6 +511,9 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
 //   APPLY          theta <- R_T(R_T(R_T(theta - theta0) * alpha) + theta0)   trainer.py:428-436
 //   REVERSE        theta <- R_T(R_T(R_T(theta - theta0) / alpha) + theta0)   trainer.py:447-451
 //   REVERSE_SUMSQ  REVERSE, then partial[c] of the new theta (next norm, trainer.py:455-457)
+//   APPLY_F32      theta <- R_T(fp32(R_T(theta - theta0)) * alpha + theta0) with an fp32 alpha:
+//                  the first-order path's apply (trainer.py:428-436 with gamma an fp32
+//                  Parameter, so v and temp stay fp32 and copy_ rounds once)
 // One chunk per workgroup; squares and sums in fp64 (exact squares of the
 // fp32-widened differences); fixed reduction order, so results are deterministic.
 // ---------------------------------------------------------------------------
@@ -529,6 +532,8 @@ __device__ __forceinline__ void proj_elem(int mode, uint32_t thb, uint32_t t0b, 
   float v;
   if (mode == kProjApply) {
     v = rt<DT>(d * alpha);
+  } else if (mode == kProjApplyF32) {
+    v = d * alpha;
   } else {
     v = rt<DT>(d / alpha);
   }
@@ -564,7 +569,11 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
   const DzChunk ch = chunks[c];
   const uint32_t grp = ch.meta & kDzMetaGroupMask;
   float alpha = 0.0f;
-  if constexpr (MODE != kProjSumsq) alpha = DT_<DT>::to_f((uint32_t)((const S*)alpha_T)[grp]);
+  if constexpr (MODE == kProjApplyF32) {
+    alpha = ((const float*)alpha_T)[grp];
+  } else if constexpr (MODE != kProjSumsq) {
+    alpha = DT_<DT>::to_f((uint32_t)((const S*)alpha_T)[grp]);
+  }
   char* tp = (char*)ch.ptr;
   const char* ap = (const char*)ch.aux;
   double acc = 0.0;
@@ -615,14 +624,41 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
   }
 }
 
-// Per-group reduction of chunk partials, in chunk order, then
-// norm = R_T(sqrt_f32(fp32(sum)))  (torch.norm: fp32 accumulate, fp32 sqrt, cast to T).
+// Per-group dot products with other tensors of the same shapes:
+//   partial[c] = sum over chunk of fp32(other) * fp32(R_T(theta - theta0))
+// (fp64 products of fp32 values are exact; fp64 sums). The gradient of the
+// first-order objective with respect to alpha: trainer.py:428-429 under
+// autograd gives sum(fp32(grad theta') * fp32(delta)) per projected tensor.
+template <int DT>
+__global__ void __launch_bounds__(kProjThreads) dot_kernel(const DzChunk* __restrict__ chunks, DzPtrArray other,
+                                                           double* __restrict__ partials) {
+  using S = typename DT_<DT>::S;
+  constexpr int kES = (int)sizeof(S);
+  __shared__ double red[kProjThreads / 64];
+  const uint32_t c = blockIdx.x;
+  const DzChunk ch = chunks[c];
+  const uint32_t grp = ch.meta & kDzMetaGroupMask;
+  const S* tp = (const S*)ch.ptr;
+  const S* ap = (const S*)ch.aux;
+  const S* op = (const S*)(other.p[grp] + ch.zgroup * (uint64_t)kES);
+  double acc = 0.0;
+  for (uint32_t e = threadIdx.x; e < ch.n; e += kProjThreads) {
+    const float d = rt<DT>(DT_<DT>::to_f((uint32_t)tp[e]) - DT_<DT>::to_f((uint32_t)ap[e]));
+    acc += (double)DT_<DT>::to_f((uint32_t)op[e]) * (double)d;
+  }
+  const double t = block_sum_f64(acc, red);
+  if (threadIdx.x == 0) partials[c] = t;
+}
+
+// Per-group reduction of chunk partials, in chunk order. With take_sqrt:
+// norm = R_T(sqrt_f32(fp32(sum)))  (torch.norm: fp32 accumulate, fp32 sqrt, cast to T);
+// without: the fp32 / T outputs hold the rounded sum itself.
 template <int DT>
 __global__ void __launch_bounds__(kProjThreads) finalize_kernel(const double* __restrict__ partials,
                                                                 const uint32_t* __restrict__ gbegin,
                                                                 double* __restrict__ sumsq,
                                                                 float* __restrict__ norm_f32,
-                                                                void* __restrict__ norm_T) {
+                                                                void* __restrict__ norm_T, bool take_sqrt) {
   using S = typename DT_<DT>::S;
   __shared__ double red[kProjThreads / 64];
   const uint32_t g = blockIdx.x;
@@ -632,7 +668,7 @@ __global__ void __launch_bounds__(kProjThreads) finalize_kernel(const double* __
   const double t = block_sum_f64(x, red);
   if (threadIdx.x == 0) {
     // correctly rounded fp32 sqrt of the fp32 sum (a double sqrt rounds once more, exactly)
-    const float n = (float)sqrt((double)(float)t);
+    const float n = take_sqrt ? (float)sqrt((double)(float)t) : (float)t;
     if (sumsq) sumsq[g] = t;
     if (norm_f32) norm_f32[g] = n;
     if (norm_T) ((S*)norm_T)[g] = (S)DT_<DT>::from_f(n);
@@ -728,6 +764,10 @@ static hipError_t launch_proj_dt(int mode, const DzChunk* chunks, uint32_t nchun
       hipLaunchKernelGGL((proj_kernel<DT, kProjReverseSumsq>), dim3(nchunks), dim3(kProjThreads),
                          0, st, chunks, alpha, partials);
       break;
+    case kProjApplyF32:
+      hipLaunchKernelGGL((proj_kernel<DT, kProjApplyF32>), dim3(nchunks), dim3(kProjThreads), 0,
+                         st, chunks, alpha, partials);
+      break;
     default:
       return hipErrorInvalidValue;
   }
@@ -744,20 +784,38 @@ hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchu
   }
 }
 
+hipError_t launch_dot(int dtype, const DzChunk* chunks, uint32_t nchunks, const DzPtrArray& other,
+                      double* partials, hipStream_t st) {
+  switch (dtype) {
+    case DZ_F32:
+      hipLaunchKernelGGL((dot_kernel<DZ_F32>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other, partials);
+      break;
+    case DZ_F16:
+      hipLaunchKernelGGL((dot_kernel<DZ_F16>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other, partials);
+      break;
+    case DZ_BF16:
+      hipLaunchKernelGGL((dot_kernel<DZ_BF16>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other, partials);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_finalize(int dtype, const double* partials, const uint32_t* gbegin, uint32_t ngroups,
-                           double* sumsq, float* norm_f32, void* norm_T, hipStream_t st) {
+                           double* sumsq, float* norm_f32, void* norm_T, bool take_sqrt, hipStream_t st) {
   switch (dtype) {
     case DZ_F32:
       hipLaunchKernelGGL((finalize_kernel<DZ_F32>), dim3(ngroups), dim3(kProjThreads), 0, st,
-                         partials, gbegin, sumsq, norm_f32, norm_T);
+                         partials, gbegin, sumsq, norm_f32, norm_T, take_sqrt);
       break;
     case DZ_F16:
       hipLaunchKernelGGL((finalize_kernel<DZ_F16>), dim3(ngroups), dim3(kProjThreads), 0, st,
-                         partials, gbegin, sumsq, norm_f32, norm_T);
+                         partials, gbegin, sumsq, norm_f32, norm_T, take_sqrt);
       break;
     case DZ_BF16:
       hipLaunchKernelGGL((finalize_kernel<DZ_BF16>), dim3(ngroups), dim3(kProjThreads), 0, st,
-                         partials, gbegin, sumsq, norm_f32, norm_T);
+                         partials, gbegin, sumsq, norm_f32, norm_T, take_sqrt);
       break;
     default:
       return hipErrorInvalidValue;

@@ -23,13 +23,26 @@ gamma, the norms and alpha (clip, SPSA step, ratio) is evaluated elementwise
 over a (G,) tensor with the reference's expressions, which gives each group
 the reference's value.
 
+The first-order path (``ENHANCED=fo``: ``DiZO.forward``, trainer.py:714-741,
+and ``dizo_iters``, trainer.py:805-830) applies the projection in place with
+an fp32 alpha (the reference's gamma is an fp32 Parameter there, so the
+projected value is rounded to the model dtype once) inside an autograd
+Function, runs the model forward with the graph, and in backward reduces
+sum(fp32(dL/dtheta') * fp32(Delta)) per group with one kernel launch; the
+tensors are then restored from a snapshot, because the reference evaluates
+every iteration on a deep copy and never changes the model during the
+search. Adam on gamma is torch's, as in the reference.
+
 Differences from the reference, by design:
   * gamma noise (torch.normal in perturb_gamma, trainer.py:554) comes from
     the library's generator: stream DZ_STREAM_GAMMA keyed by the seed of the
     ZO step that triggered the event, one draw of G normals per SPSA
     iteration (``gamma_seed`` / draw counter);
   * norms accumulate in fp64 and round once (torch.norm accumulates in fp32):
-    within one unit in the last place of the model dtype.
+    within one unit in the last place of the model dtype; likewise the
+    first-order gradient's per-group sums (fp64 instead of fp32);
+  * the first-order path works on the model itself (projected tensors
+    snapshotted and restored) instead of a deep copy of the whole model.
 """
 from __future__ import annotations
 
@@ -41,13 +54,49 @@ from torch import nn
 from . import _lib as L
 from ._lib import DzError
 from .table import ProjTable, normals
-from .trainer import forward_wrap_with_option_len
+from .trainer import forward_wrap_with_option_len, option_len_loss
 
 TAU, GAMMA_EPS, STEP_SIZE = 0.2, 0.1, 2  # trainer.py:590-592
 
 
+class _ApplyFO(torch.autograd.Function):
+    """theta' = R_T(fp32(R_T(theta - theta0)) * alpha + theta0), alpha = gamma / (norm + 1e-8),
+    written in place into the projected tensors and recorded for autograd, as
+    the reference's copy_ into the copied model records it (trainer.py:428-436
+    under DiZO.forward, trainer.py:714-741)."""
+
+    @staticmethod
+    def forward(ctx, dizo, tab, saved_tab, norms, *args):
+        G = dizo.G
+        gammas, params = args[:G], args[G:]
+        gam = torch.cat([g.detach().reshape(1) for g in gammas])
+        denom = norms + 1e-8  # in the model dtype, as the reference's norms + 1e-8
+        alpha = (gam / denom).contiguous()
+        dizo._apply_alpha(tab, alpha)
+        ctx.mark_dirty(*params)
+        ctx.saved_tab = saved_tab
+        ctx.save_for_backward(denom)
+        return tuple(params)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        (denom,) = ctx.saved_tensors
+        tab = ctx.saved_tab
+        gs = [torch.zeros_like(t) if g is None else g.to(t.dtype).contiguous() for g, t in zip(grads, tab.tensors)]
+        dot = torch.empty(len(gs), dtype=torch.float32, device=denom.device)
+        tab.group_dot(gs, dot_f32=dot)  # dL/dalpha per group
+        grad_gamma = dot / denom.to(torch.float32)  # d(gamma / denom) / d gamma
+        return (None, None, None, None) + tuple(grad_gamma[i:i + 1] for i in range(len(gs))) + (None,) * len(gs)
+
+
 class DiZO(nn.Module):
     """One gamma per projected tensor and the projection passes (trainer.py:378-614)."""
+
+    @staticmethod
+    def forward_wrap_with_option_len(self, input_ids=None, labels=None, option_len=None, num_options=None,
+                                     return_dict=None, **kwargs):
+        """trainer.py:470-542: the loss with the forward's autograd graph (``self`` is the model)."""
+        return option_len_loss(self, True, input_ids, labels, option_len, num_options, return_dict, **kwargs)
 
     def __init__(self, model, norm_mode, exclude_list=[]) -> None:  # noqa: B006 (reference signature)
         super().__init__()
@@ -89,6 +138,11 @@ class DiZO(nn.Module):
         self._norms: Optional[torch.Tensor] = None  # norms of the current theta - theta0, when known
         self._in_event = False  # the driver vouches that theta is unchanged since _norms
         self.kernel_timer = None
+        # first-order path: snapshot of the projected tensors and its table
+        self._fo_saved: Optional[List[torch.Tensor]] = None
+        self._fo_tab: Optional[ProjTable] = None
+        self._fo_params: Optional[List[torch.Tensor]] = None
+        self._fo_dirty = False
 
     # ---------------------------------------------------------- gamma ----
     @property
@@ -143,11 +197,16 @@ class DiZO(nn.Module):
         return self._gamma / (norms + 1e-8)
 
     def _apply_alpha(self, tab: ProjTable, alpha: torch.Tensor) -> None:
-        if alpha.dtype != tab.dtype:
-            raise DzError(f"DiZO: alpha is {alpha.dtype} but the projected tensors are {tab.dtype} "
-                          "(a float32 gamma is the first-order path, dizo_iters)")
+        """Alpha in the model dtype (gamma in T, the ZO path): R(R(Delta alpha) + theta0);
+        fp32 alpha (fp32 gamma, the first-order path): one rounding at the end."""
         alpha = alpha.contiguous()
-        self._timed("proj_apply", tab, 3, lambda: tab.project(alpha, L.DZ_PROJ_APPLY))
+        if alpha.dtype == tab.dtype:
+            mode = L.DZ_PROJ_APPLY
+        elif alpha.dtype == torch.float32:
+            mode = L.DZ_PROJ_APPLY_F32ALPHA
+        else:
+            raise DzError(f"DiZO: alpha is {alpha.dtype} but the projected tensors are {tab.dtype}")
+        self._timed("proj_apply", tab, 3, lambda: tab.project(alpha, mode))
         self._alpha_vec = alpha
         self._norms = None
         self.alpha = {name: alpha[i:i + 1] for i, name in enumerate(self.constraints_name)}
@@ -157,6 +216,8 @@ class DiZO(nn.Module):
         """trainer.py:447-451 for every group, returning the norms of the reversed theta."""
         if self._alpha_vec is None:
             raise DzError("DiZO: reverse_constraints before apply_constraints")
+        if self._alpha_vec.dtype != tab.dtype:
+            raise DzError("DiZO: reverse_constraints after an fp32-alpha (first-order) apply is not supported")
         norms = torch.empty(self.G, dtype=tab.dtype, device=tab.device)
         self._timed("proj_reverse_sumsq", tab, 3,
                     lambda: tab.project(self._alpha_vec, L.DZ_PROJ_REVERSE_SUMSQ, norm_T=norms))
@@ -247,14 +308,60 @@ class DiZO(nn.Module):
         self.ts = [ts_v[i] for i in range(self.G)]
         self.last_losses = (loss1, loss2)
 
+    # ------------------------------------------------ first-order path --
+    def _fo_snapshot(self, new, pre_trained):
+        """Copies the projected tensors into the snapshot (allocated once)."""
+        params = dict(new.named_parameters())
+        anchors = dict(pre_trained.named_parameters())
+        ps = [params[n] for n in self.constraints_name]
+        if self._fo_saved is None or any(a.shape != b.shape for a, b in zip(self._fo_saved, ps)):
+            if self._fo_tab is not None:
+                self._fo_tab.close()
+            self._fo_saved = [torch.empty_like(p.data) for p in ps]
+            self._fo_tab = ProjTable(self._fo_saved, [anchors[n].data for n in self.constraints_name])
+        with torch.no_grad():
+            for b, p in zip(self._fo_saved, ps):
+                b.copy_(p.data)
+        self._fo_params = ps
+        return ps
+
+    def fo_restore(self) -> None:
+        """Puts the projected tensors back to the snapshot after a first-order
+        iteration and drops their autograd history."""
+        if self._fo_dirty:
+            with torch.no_grad():
+                for p, b in zip(self._fo_params, self._fo_saved):
+                    p.detach_()
+                    p.requires_grad_(False)
+                    p.data.copy_(b)
+            self._fo_dirty = False
+            self._norms = None
+
     def forward(self, new=None, pre_trained=None, x=None, apply=False):
-        """trainer.py:714-741 (first-order gamma objective)."""
-        raise NotImplementedError("DiZO first-order objective (ENHANCED=fo) is not implemented yet")
+        """trainer.py:714-741: with apply, the final projection; otherwise the
+        first-order objective loss + 1e-3 * sum |gamma| on the projected model,
+        differentiable with respect to gamma."""
+        self.fo_restore()
+        if apply:
+            self.apply_constraints(new, pre_trained, iter(self.constraints), apply=True)
+            return None
+        tab = self._table(new, pre_trained)
+        params = self._fo_snapshot(new, pre_trained)
+        norms = self._group_norms(tab)
+        self._freeze(new)
+        _ApplyFO.apply(self, tab, self._fo_tab, norms, *list(self.constraints), *params)
+        self._fo_dirty = True
+        self._norms = None
+        out = self.forward_wrap_with_option_len(new, **x, return_dict=True)
+        return out.loss + 1e-3 * sum(p.abs().sum() for p in self.constraints.parameters())
 
     def close(self) -> None:
-        if self._tab is not None:
-            self._tab.close()
-            self._tab = None
+        self.fo_restore()
+        for name in ("_tab", "_fo_tab"):
+            tab = getattr(self, name)
+            if tab is not None:
+                tab.close()
+                setattr(self, name, None)
 
 
 class dizo_trainer:  # noqa: N801 (reference name)
@@ -311,8 +418,22 @@ class dizo_trainer:  # noqa: N801 (reference name)
         self.i += 1
 
     def dizo_iters(self, model, base_model, apply=False):
-        """trainer.py:805-830 (first-order gamma search)."""
-        raise NotImplementedError("DiZO first-order gamma search (ENHANCED=fo) is not implemented yet")
+        """trainer.py:805-830: max_iters first-order iterations (Adam on gamma,
+        lr proj_lr), then the final apply."""
+        dz = self.dizo
+        if not apply:
+            self.count = 0
+            with torch.enable_grad():
+                while self.count < self.max_iters:
+                    data = self._next_batch()
+                    pgm_loss = dz(model, base_model, x=data)
+                    self.pgm_optimizer.zero_grad()
+                    pgm_loss.backward()
+                    self.pgm_optimizer.step()
+                    dz.fo_restore()
+                    self.count += 1
+        dz(model, self.pre_trained, apply=True)
+        self.i += 1
 
     def close(self) -> None:
         self.dizo.close()

@@ -190,13 +190,29 @@ class ProjTable(_Table):
 
     def project(self, alpha: torch.Tensor, mode: int, sumsq=None, norm_f32=None, norm_T=None, *,
                 stream=None) -> None:
-        """APPLY (trainer.py:428-436) / REVERSE (trainer.py:447-451) with per-group alpha."""
-        if alpha.dtype != self.dtype or alpha.device != self.device or alpha.numel() != self.n \
+        """APPLY (trainer.py:428-436) / REVERSE (trainer.py:447-451) with per-group alpha
+        (alpha in the table dtype; float32 for APPLY_F32ALPHA)."""
+        want = torch.float32 if mode == L.DZ_PROJ_APPLY_F32ALPHA else self.dtype
+        if alpha.dtype != want or alpha.device != self.device or alpha.numel() != self.n \
                 or not alpha.is_contiguous():
-            raise DzError(f"alpha must be a contiguous {self.dtype} tensor of {self.n} values on {self.device}")
+            raise DzError(f"alpha must be a contiguous {want} tensor of {self.n} values on {self.device}")
         self._outs(sumsq, norm_f32, norm_T)
         L.call("dz_project", self.handle, alpha.data_ptr(), int(mode), _ptr(sumsq), _ptr(norm_f32),
                _ptr(norm_T), stream_handle(stream))
+
+
+    def group_dot(self, others, dot=None, dot_f32=None, *, stream=None) -> None:
+        """Per group: sum fp32(other) * fp32(R(theta - theta0)), others shaped like the tensors."""
+        others = list(others)
+        if len(others) != self.n:
+            raise DzError(f"group_dot: {len(others)} tensors for {self.n} groups")
+        for i, (o, t) in enumerate(zip(others, self.tensors)):
+            if o.dtype != self.dtype or o.device != self.device or o.numel() != t.numel() or not o.is_contiguous():
+                raise DzError(f"group_dot: tensor {i} must be a contiguous {self.dtype} tensor of {t.numel()} "
+                              f"values on {self.device}")
+        self._outs(dot, dot_f32, None)
+        L.call("dz_group_dot", self.handle, L.u64_array([o.data_ptr() for o in others]), _ptr(dot),
+               _ptr(dot_f32), stream_handle(stream))
 
 
 def normals(seed: int, stream_id: int, offset: int, n: int, dtype: torch.dtype,

@@ -106,9 +106,11 @@ def select_trainable(model: torch.nn.Module) -> Tuple[List[Tuple[str, torch.nn.P
     return named, exclude
 
 
-def forward_wrap_with_option_len(self, input_ids=None, labels=None, option_len=None, num_options=None,
-                                 return_dict=None, **kwargs):
-    """The option-masked classification loss of trainer.py:1446-1522 (``self`` is the model).
+def option_len_loss(model, build_graph: bool, input_ids=None, labels=None, option_len=None, num_options=None,
+                    return_dict=None, **kwargs):
+    """The option-masked classification loss of trainer.py:1446-1522 (and of its
+    copy in DiZO, trainer.py:470-542, which differs only by building the
+    autograd graph: build_graph=True).
 
     Same torch operations in the same order, so the loss (in the model dtype)
     is the reference's for the same logits. The per-example masking loop of
@@ -119,14 +121,17 @@ def forward_wrap_with_option_len(self, input_ids=None, labels=None, option_len=N
     concatenations per layer; the logits are the same.
     """
     kwargs.setdefault("use_cache", False)
-    with torch.no_grad():
-        outputs = self.forward(input_ids=input_ids, **kwargs)
+    if build_graph:
+        outputs = model.forward(input_ids=input_ids, **kwargs)
+    else:
+        with torch.no_grad():
+            outputs = model.forward(input_ids=input_ids, **kwargs)
     if labels is None:
         return outputs
     logits = outputs.logits
     shift_logits = logits[..., :-1, :].contiguous()
     shift_labels = torch.clone(input_ids)[..., 1:].contiguous()
-    shift_labels[shift_labels == self.config.pad_token_id] = -100
+    shift_labels[shift_labels == model.config.pad_token_id] = -100
     if option_len is not None:
         ol = torch.as_tensor(option_len, device=shift_labels.device).reshape(-1, 1)
         pos = torch.arange(shift_labels.shape[1], device=shift_labels.device).reshape(1, -1)
@@ -151,10 +156,16 @@ def forward_wrap_with_option_len(self, input_ids=None, labels=None, option_len=N
             selected = selected.view(-1, nopt[0])
             loss = loss_fct(selected, labels.view(-1, nopt[0])[:, 0])
     else:
-        loss = loss_fct(shift_logits.view(-1, self.config.vocab_size), shift_labels.view(-1))
+        loss = loss_fct(shift_logits.view(-1, model.config.vocab_size), shift_labels.view(-1))
     if not return_dict:
         return (loss, logits) + tuple(outputs[1:])
     return SimpleNamespace(loss=loss)
+
+
+def forward_wrap_with_option_len(self, input_ids=None, labels=None, option_len=None, num_options=None,
+                                 return_dict=None, **kwargs):
+    """trainer.py:1446-1522 (``self`` is the model): the ZO forward's loss, no autograd graph."""
+    return option_len_loss(self, False, input_ids, labels, option_len, num_options, return_dict, **kwargs)
 
 
 class _ZOTables:

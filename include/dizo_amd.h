@@ -34,6 +34,7 @@ extern "C" {
 #define DZ_PROJ_APPLY 1         /* theta <- theta0 + (theta - theta0) * alpha  */
 #define DZ_PROJ_REVERSE 2       /* theta <- theta0 + (theta - theta0) / alpha  */
 #define DZ_PROJ_REVERSE_SUMSQ 3 /* REVERSE, then the norms of the new theta    */
+#define DZ_PROJ_APPLY_F32ALPHA 4 /* APPLY with an fp32 alpha, one final rounding */
 
 #define DZ_STREAM_PARAM 0u /* z of parameter perturbation / update */
 #define DZ_STREAM_GAMMA 1u /* z of the DiZO gamma perturbation     */
@@ -143,6 +144,17 @@ int32_t dz_group_sumsq(dz_table* t, double* d_sumsq, float* d_norm_f32, void* d_
  * theta (the next _project_ratio, trainer.py:455-457) to the outputs. */
 int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sumsq,
                    float* d_norm_f32, void* d_norm_T, void* stream);
+/* (mode DZ_PROJ_APPLY_F32ALPHA takes one fp32 alpha per group and computes
+ * theta <- R_T(fp32(R_T(theta - theta0)) * alpha + theta0): apply_constraints
+ * with the fp32 gamma of the first-order path, trainer.py:428-436, 714-741.) */
+
+/* Per group g: d_dot[g] = sum fp32(other_g) * fp32(R_T(theta_g - theta0_g))
+ * (fp64 accumulation; d_dot_f32[g] its fp32 rounding), with other_ptrs a host
+ * array of n device addresses of tensors shaped like theta_g (n <= 128). The
+ * gradient of the first-order gamma objective with respect to alpha
+ * (autograd through trainer.py:428-429 in DiZO.forward, trainer.py:714-741). */
+int32_t dz_group_dot(dz_table* t, const uint64_t* other_ptrs, double* d_dot, float* d_dot_f32,
+                     void* stream);
 
 #ifdef __cplusplus
 }

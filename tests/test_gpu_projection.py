@@ -121,3 +121,42 @@ def test_empty_and_rejects():
     with pytest.raises(DzError):
         ProjTable(a, [torch.zeros(0, device=dev), torch.zeros(11, device=dev)])
     tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_apply_f32_alpha_matches_torch(dt):
+    """APPLY_F32ALPHA: the reference's apply with an fp32 gamma (first-order path):
+    (theta - theta0) * alpha + theta0 with alpha float32 of shape (1,), copied into T."""
+    from dizo_amd._lib import DZ_PROJ_APPLY_F32ALPHA
+    from dizo_amd.table import ProjTable
+    ths, t0s, _, _ = _groups(dt, 13, sizes=[8192, 4099, 70000, 7])
+    ref = [t.clone() for t in ths]
+    G = len(ths)
+    alphas = torch.tensor(np.linspace(0.5, 1.3, G), dtype=torch.float32, device=ths[0].device)
+    tab = ProjTable(ths, t0s)
+    tab.project(alphas, DZ_PROJ_APPLY_F32ALPHA)
+    for g in range(G):
+        want = ((ref[g] - t0s[g]) * alphas[g:g + 1] + t0s[g]).to(DT_TORCH[dt])
+        assert_bits_equal(to_bits(ths[g]), to_bits(want), dt, f"apply_f32 group {g}")
+    tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_group_dot_matches_fp64(dt):
+    """group_dot: sum fp32(other) * fp32(R(theta - theta0)) per group, fp64 accumulation,
+    against the same sum formed in float64 by torch (up to summation order)."""
+    from dizo_amd.table import ProjTable
+    ths, t0s, _, _ = _groups(dt, 21, sizes=[8192, 8191, 300000, 5, 0])
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    others = [torch.randn(t.numel(), device=t.device, generator=gen).to(DT_TORCH[dt]) for t in ths]
+    G = len(ths)
+    dot = torch.empty(G, dtype=torch.float64, device=ths[0].device)
+    dotf = torch.empty(G, dtype=torch.float32, device=ths[0].device)
+    tab = ProjTable(ths, t0s)
+    tab.group_dot(others, dot, dotf)
+    for g in range(G):
+        delta = (ths[g] - t0s[g]).double()
+        want = float((others[g].double() * delta).sum())
+        assert float(dot[g]) == pytest.approx(want, rel=1e-12, abs=1e-300)
+        assert float(dotf[g]) == np.float32(float(dot[g]))
+    tab.close()
