@@ -65,7 +65,7 @@ def load_traffic(kernel: str, workload: str):
         return None
 
 
-def run_steps(wl_name: str, steps: int, warmup: int, log=print):
+def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = False):
     import numpy as np
     import torch
 
@@ -83,7 +83,7 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print):
     torch.cuda.synchronize()
     log(f"[bench] built {shape.name} {dtype} + anchor in {time.perf_counter() - t0:.1f}s; "
         f"mem {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
-    args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=warmup + steps, enhanced="zo")
+    args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=warmup + steps, enhanced="zo", zo_graph=graph)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches), base_model=base)
     P = sum(p.numel() for _, p in tr.named_parameters_to_optim)
@@ -237,6 +237,7 @@ def main(argv=None):
     ap.add_argument("--workload", default="c4", choices=sorted(WORKLOADS))
     ap.add_argument("--kernels", action="store_true", help="per-pass kernel microbench instead of full steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true", help="replay each ZO step as a captured hipGraph")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the DiZO step path is measured on a "
@@ -259,7 +260,7 @@ def main(argv=None):
         res = kernel_microbench(a.workload, log=log)
         print(json.dumps({"metric": "ZO pass HBM GB/s", "workload": a.workload, **res}), flush=True)
         return 0
-    r = run_steps(a.workload, a.steps, a.warmup, log=log)
+    r = run_steps(a.workload, a.steps, a.warmup, log=log, graph=a.graph)
     wl = WORKLOADS[a.workload]
     value = a.steps / r["elapsed"]
     summ = r["summary"]
@@ -267,8 +268,8 @@ def main(argv=None):
     rmw_bytes = sum(s["bytes_per_launch"] * s["launches"] for s in rmw)
     rmw_ms = sum(s["total_ms"] for s in rmw)
     rmw_launches = sum(s["launches"] for s in rmw)
-    achieved = rmw_bytes / (rmw_ms * 1e-3) / 1e9
-    mean_ms = rmw_ms / rmw_launches
+    achieved = rmw_bytes / (rmw_ms * 1e-3) / 1e9 if rmw_ms else None
+    mean_ms = rmw_ms / rmw_launches if rmw_launches else None
     line = {
         "metric": "ZO steps/sec at OPT-13B fp16" if a.workload == "c4" else f"ZO steps/sec ({a.workload})",
         "value": value,
@@ -293,9 +294,9 @@ def main(argv=None):
             "achieved": achieved,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBPS,
+            "frac": achieved / HBM_PEAK_GBPS if achieved else None,
             "traffic": load_traffic("rmw_kernel", a.workload),
-            "algorithmic_bytes_per_launch": rmw_bytes / rmw_launches,
+            "algorithmic_bytes_per_launch": rmw_bytes / rmw_launches if rmw_launches else None,
             "mean_launch_ms": mean_ms,
             "launches_per_step": rmw_launches / a.steps,
         },

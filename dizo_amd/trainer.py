@@ -76,6 +76,8 @@ class ZOArguments:
     # the first perturbation of the next zo_step
     zo_fuse_restore: bool = True
     zo_fuse_next_perturb: bool = True
+    # build-specific: replay each step as a captured hipGraph (ZOTrainer only)
+    zo_graph: bool = False
 
 
 def layout_z_offsets(numels: Sequence[int]) -> List[int]:
@@ -131,19 +133,22 @@ def option_len_loss(model, build_graph: bool, input_ids=None, labels=None, optio
     logits = outputs.logits
     shift_logits = logits[..., :-1, :].contiguous()
     shift_labels = torch.clone(input_ids)[..., 1:].contiguous()
-    shift_labels[shift_labels == model.config.pad_token_id] = -100
+    # masked_fill_ sets the same elements as the reference's boolean-index
+    # assignments without a device-to-host sync (so the loss can be captured)
+    shift_labels.masked_fill_(shift_labels == model.config.pad_token_id, -100)
     if option_len is not None:
         ol = torch.as_tensor(option_len, device=shift_labels.device).reshape(-1, 1)
         pos = torch.arange(shift_labels.shape[1], device=shift_labels.device).reshape(1, -1)
-        shift_labels[pos < shift_labels.shape[1] - ol] = -100
+        shift_labels.masked_fill_(pos < shift_labels.shape[1] - ol, -100)
     loss_fct = CrossEntropyLoss(ignore_index=-100)
     if num_options is not None:
         log_probs = F.log_softmax(shift_logits, dim=-1)
         mask = shift_labels != -100
-        shift_labels[~mask] = 0
+        shift_labels.masked_fill_(~mask, 0)
         selected = torch.gather(log_probs, dim=-1, index=shift_labels.unsqueeze(-1)).squeeze(-1)
         selected = (selected * mask).sum(-1) / mask.sum(-1)
-        nopt = [int(x) for x in num_options]
+        # a host list of option counts avoids a sync; a tensor is read back
+        nopt = [int(x) for x in (num_options.tolist() if torch.is_tensor(num_options) else num_options)]
         if any(x != nopt[0] for x in nopt):
             loss, start, count = 0, 0, 0
             while start < len(nopt):
@@ -268,6 +273,11 @@ class ZOTrainerMixin:
     def zo_flush(self) -> None:
         """Applies deferred work: a pending restore+update, or a pending restore
         (the +1 perturbation that ends zo_step)."""
+        graph = getattr(self, "_graph", None)
+        if graph is not None:
+            if graph.capturing:
+                return  # the captured step manages the parameters itself
+            graph.flush()
         pu = self._pending_update
         if pu is not None:
             self._pending_update = None
@@ -373,6 +383,9 @@ class ZOTrainerMixin:
 
     def zo_close(self) -> None:
         self.zo_flush()
+        if getattr(self, "_graph", None) is not None:
+            self._graph.close()
+            self._graph = None
         if self._zo_tabs is not None:
             self._zo_tabs.close()
             self._zo_tabs = None
@@ -410,22 +423,59 @@ class ZOTrainer(ZOTrainerMixin):
         self.zo_setup(model, train_dataloader, base_model=base_model)
         self.tr_loss = torch.zeros((), device=self.named_parameters_to_optim[0][1].device)
         self._last_logged = 0
+        self._graph = None
+        if getattr(args, "zo_graph", False):
+            from .graph import GraphedZOStep
 
-    def training_step(self, inputs) -> torch.Tensor:
-        """One optimisation step (trainer.py:1224-1326 with gradient_accumulation_steps = 1)."""
-        model = self.model
-        tr_loss_step = self.zo_step(model, inputs)
-        if self.args.logging_nan_inf_filter and (torch.isnan(tr_loss_step) or torch.isinf(tr_loss_step)):
-            self.tr_loss += self.tr_loss / (1 + self.state.global_step - self._last_logged)
+            self._graph = GraphedZOStep(self)
+
+    def _account(self, tr_loss_step) -> None:
+        """The loss bookkeeping of trainer.py:1242-1250 (NaN/inf filter) on the device."""
+        if self.args.logging_nan_inf_filter:
+            bad = ~torch.isfinite(tr_loss_step)
+            dec = self.tr_loss / (1 + self.state.global_step - self._last_logged)
+            self.tr_loss = torch.where(bad, self.tr_loss + dec, self.tr_loss + tr_loss_step)
         else:
-            self.tr_loss += tr_loss_step
-        self.zo_update(self.args, model)
+            self.tr_loss = self.tr_loss + tr_loss_step
+
+    def _finish_step(self, tr_loss_step) -> None:
         self.state.global_step += 1
         if self.state.global_step % DIZO_INTERVAL == 0:
             self.state.log_history.append({"loss": round(tr_loss_step.item(), 4),
                                            "lr": self._get_learning_rate(),
                                            "step": self.state.global_step})
         self.loss_list.append(tr_loss_step)
+
+    def training_step(self, inputs) -> torch.Tensor:
+        """One optimisation step (trainer.py:1224-1326 with gradient_accumulation_steps = 1)."""
+        if self._graph is not None:
+            return self._graph_step(inputs)
+        model = self.model
+        tr_loss_step = self.zo_step(model, inputs)
+        self._account(tr_loss_step)
+        self.zo_update(self.args, model)
+        self._finish_step(tr_loss_step)
+        return tr_loss_step
+
+    def _graph_step(self, inputs) -> torch.Tensor:
+        """The same step replayed as a captured graph: zo_step and the update of
+        zo_update with the seed, gradient and learning rate kept on the device
+        (projected_grad is not read back; it stays None)."""
+        args = self.args
+        self.zo_random_seed = np.random.randint(1000000000)
+        lr = self._get_learning_rate()
+        tr_loss_step = self._graph.step(inputs, self.zo_random_seed, lr).clone()
+        self.projected_grad = None
+        self._account(tr_loss_step)
+        if (self.state.global_step + 1) % DIZO_INTERVAL == 0 and args.enhanced:
+            self.zo_flush()
+            self.dizo_trainer.gamma_seed = self.zo_random_seed
+            if args.enhanced == "zo":
+                self.dizo_trainer.dizo_zo_iters(self.model, base_model=self.base_model)
+            else:
+                self.dizo_trainer.dizo_iters(self.model, base_model=self.base_model)
+        self.lr_scheduler.step()
+        self._finish_step(tr_loss_step)
         return tr_loss_step
 
     def train(self, batches, max_steps: Optional[int] = None):

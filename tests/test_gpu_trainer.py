@@ -263,3 +263,43 @@ def test_dizo_first_order_event_matches_reference(dt):
     g_torch, _ = _ref_fo_event(model_c, copy.deepcopy(anchor_b), names, batches, exact_dot=False)
     assert torch.allclose(g_lib, g_torch, rtol=5e-2, atol=1e-4), f"gamma {g_lib} vs torch fp32 {g_torch}"
     dtr.close()
+
+
+def _run_trainer(dt, graph, enhanced, steps, batches, seed=31):
+    from dizo_amd.synth import Cycle, build_opt
+    from dizo_amd.trainer import ZOArguments, ZOTrainer
+    model = build_opt("opt-tiny", dt, "cuda", seed=seed)
+    args = ZOArguments(learning_rate=1e-3, zo_eps=1e-3, max_steps=steps, enhanced=enhanced, zo_graph=graph)
+    np.random.seed(26)
+    tr = ZOTrainer(model, args, train_dataloader=Cycle(batches))
+    it = iter(Cycle(batches))
+    losses = [tr.training_step(next(it)) for _ in range(steps)]
+    tr.zo_close()
+    torch.cuda.synchronize()
+    return torch.stack([l.reshape(()) for l in losses]), [p.detach().clone() for p in model.parameters()]
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_graph_steps_match_eager(dt):
+    """Captured-graph steps (two input shapes with padding, one unpadded shape,
+    each replayed several times) give the eager path's losses and parameters
+    bit for bit."""
+    from dizo_amd.synth import make_batches
+    padded = make_batches(4, 4, 512, seed=41, device="cuda", min_len=8, max_len=20)
+    fixed = make_batches(2, 4, 512, seed=42, device="cuda", fixed_len=24)
+    batches = padded + fixed
+    le, pe = _run_trainer(dt, False, None, 14, batches)
+    lg, pg = _run_trainer(dt, True, None, 14, batches)
+    assert _same(le, lg), f"losses differ: {le} vs {lg}"
+    assert all(_same(a, b) for a, b in zip(pe, pg))
+
+
+def test_graph_steps_with_dizo_event_match_eager():
+    """55 steps with ENHANCED=zo: the event at global step 49 runs eagerly between
+    replays; graph and eager runs agree bit for bit."""
+    from dizo_amd.synth import make_batches
+    batches = make_batches(5, 4, 512, seed=43, device="cuda", fixed_len=16)
+    le, pe = _run_trainer(torch.float16, False, "zo", 55, batches)
+    lg, pg = _run_trainer(torch.float16, True, "zo", 55, batches)
+    assert _same(le, lg)
+    assert all(_same(a, b) for a, b in zip(pe, pg))
