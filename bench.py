@@ -6,7 +6,10 @@ forward, perturb -2, forward, fused restore+update, and every 50 steps the
 DiZO projection event with 10 SPSA iterations on gamma) on the OPT-13B fp16
 workload (config C4: 40 layers, d_model 5120, batch 16 examples x 2 candidates
 of 128 random tokens, theta0 anchor resident in HBM), synthetic random-init
-weights and synthetic token batches already resident in HBM.
+weights and synthetic token batches already resident in HBM. The loss's
+forward computes logits only at the option positions the classification loss
+reads (HF's logits_to_keep; the same loss); --full-logits computes them at
+every position as the reference does.
 
 Prints one JSON line. `roofline` is the dominant library kernel (the
 multi-tensor perturb / restore+update read-modify-write): algorithmic bytes
@@ -15,7 +18,7 @@ around every launch in the timed region. `cpu_baseline` times the
 reference's expressions (the oracle's torch restatement) on the host cores
 over a bounded sample and scales it to steps/s.
 
-  python bench.py [--gpus 1] [--steps 50] [--warmup 3] [--workload c4]
+  python bench.py [--gpus 1] [--steps 50] [--warmup 3] [--workload c4] [--graph] [--full-logits]
   python bench.py --kernels [--workload c4]     # per-pass kernel microbench (config C2 style)
 """
 from __future__ import annotations
@@ -65,7 +68,7 @@ def load_traffic(kernel: str, workload: str):
         return None
 
 
-def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = False):
+def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = False, option_head: bool = False):
     import numpy as np
     import torch
 
@@ -83,7 +86,8 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = Fa
     torch.cuda.synchronize()
     log(f"[bench] built {shape.name} {dtype} + anchor in {time.perf_counter() - t0:.1f}s; "
         f"mem {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
-    args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=warmup + steps, enhanced="zo", zo_graph=graph)
+    args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=warmup + steps, enhanced="zo", zo_graph=graph,
+                       zo_option_head=option_head)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches), base_model=base)
     P = sum(p.numel() for _, p in tr.named_parameters_to_optim)
@@ -238,6 +242,9 @@ def main(argv=None):
     ap.add_argument("--kernels", action="store_true", help="per-pass kernel microbench instead of full steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true", help="replay each ZO step as a captured hipGraph")
+    ap.add_argument("--full-logits", action="store_true",
+                    help="compute logits at every position, as the reference does (default: only at the option "
+                         "positions the loss reads, the same loss)")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the DiZO step path is measured on a "
@@ -260,7 +267,7 @@ def main(argv=None):
         res = kernel_microbench(a.workload, log=log)
         print(json.dumps({"metric": "ZO pass HBM GB/s", "workload": a.workload, **res}), flush=True)
         return 0
-    r = run_steps(a.workload, a.steps, a.warmup, log=log, graph=a.graph)
+    r = run_steps(a.workload, a.steps, a.warmup, log=log, graph=a.graph, option_head=not a.full_logits)
     wl = WORKLOADS[a.workload]
     value = a.steps / r["elapsed"]
     summ = r["summary"]
@@ -287,6 +294,7 @@ def main(argv=None):
                                f"candidates, {'seq ' + str(wl['fixed_len']) if wl['fixed_len'] else 'len U[32,64]'}, "
                                f"projection every 50 steps, theta0 resident)",
                    "zo_params": r["P"], "dizo_events_timed": r["events"], "global_batch": 2 * wl["batch"],
+                   "graph": a.graph, "option_head": not a.full_logits,
                    "seq_len": wl["fixed_len"] or wl["max_len"]},
         "roofline": {
             "kernel": "rmw_kernel (perturb -2 / restore+update / restore+update+next perturb)",

@@ -3,7 +3,8 @@
 One ZO step of the reference (trainer.py:1570-1617: perturb +1, forward,
 perturb -2, forward, projected_grad, restore, update) replays as one captured
 graph per input shape (and padded / unpadded attention mask, since the two
-take different attention paths), with no host synchronisation:
+take different attention paths, and option-head logit window), with no host
+synchronisation:
 
   first  : perturb(+1, z_k) -> forward -> perturb(-2, z_k) -> forward -> g_k
   steady : restore+update(z_{k-1}, g_{k-1}, lr_{k-1}) fused with perturb(+1, z_k)
@@ -63,6 +64,7 @@ class _Captured:
         self.static: Dict[str, torch.Tensor] = {}
         self.nopt = None
         self.unpadded = True
+        self.window = 0  # trailing positions of logits the loss reads (0: all)
         self.first: Optional[torch.cuda.CUDAGraph] = None
         self.steady: Optional[torch.cuda.CUDAGraph] = None
         self.loss1: Optional[torch.Tensor] = None  # output of `first`
@@ -110,7 +112,7 @@ class GraphedZOStep:
         with torch.inference_mode():
             kw = {k: v for k, v in st.items() if k not in ("input_ids", "labels", "option_len", "num_options")}
             return option_len_loss(model, False, st["input_ids"], st.get("labels"), st.get("option_len"),
-                                   cap.nopt, True, **kw).loss
+                                   cap.nopt, True, dz_window=cap.window, **kw).loss
 
     def _body(self, cap: _Captured, first: bool) -> torch.Tensor:
         tab, eps = self.tab, self.eps
@@ -146,9 +148,27 @@ class GraphedZOStep:
         self._pad_cache[id(am)] = (weakref.ref(am), am._version, flag)
         return flag
 
+    def _window(self, batch) -> int:
+        """The option head's logit window for this batch (0: full logits), decided
+        on the host: capture cannot read option_len back from the device."""
+        from .trainer import host_ints, option_window
+
+        if not getattr(self.tr.model, "dz_option_head", False):
+            return 0
+        if any(batch.get(k) is None for k in ("labels", "option_len", "num_options")):
+            return 0
+        return option_window(host_ints(batch["option_len"]), batch["input_ids"].shape[1]) or 0
+
     def _key(self, batch) -> Tuple:
+        """Graphs are reused for batches that agree in every tensor's shape and
+        dtype, the option counts (they choose the loss's branch), the logit
+        window and whether the mask has padding."""
+        from .trainer import host_ints
+
         shapes = tuple((k, tuple(v.shape), v.dtype) for k, v in sorted(batch.items()) if torch.is_tensor(v))
-        return shapes + (("unpadded", self._unpadded(batch)),)
+        nopt = batch.get("num_options")
+        nopt = None if nopt is None else tuple(host_ints(nopt))
+        return shapes + (("nopt", nopt), ("window", self._window(batch)), ("unpadded", self._unpadded(batch)))
 
     def _upload(self, seed: int, lr: float) -> None:
         i = self.slot
@@ -175,14 +195,17 @@ class GraphedZOStep:
             self.capturing = False
             model.config._attn_implementation = prev
 
-    def _new_capture(self, batch, unpadded: bool) -> _Captured:
+    def _new_capture(self, batch, unpadded: bool, window: int) -> _Captured:
+        from .trainer import host_ints
+
         cap = _Captured()
         for k, v in batch.items():
             if torch.is_tensor(v):
                 cap.static[k] = v.to(self.device, copy=True)
         nopt = batch.get("num_options")
-        cap.nopt = None if nopt is None else [int(x) for x in (nopt.tolist() if torch.is_tensor(nopt) else nopt)]
+        cap.nopt = None if nopt is None else list(host_ints(nopt))
         cap.unpadded = unpadded
+        cap.window = window
         return cap
 
     def _capture(self, cap: _Captured) -> None:
@@ -208,7 +231,7 @@ class GraphedZOStep:
         cap = self.caps.get(key)
         first = not self.pending
         if cap is None:
-            cap = self._new_capture(batch, key[-1][1])
+            cap = self._new_capture(batch, key[-1][1], key[-2][1])
             # one eager step through the body (warms kernels and allocator),
             # on a side stream as capture expects
             side = torch.cuda.Stream(device=self.device)

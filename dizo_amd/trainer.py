@@ -40,6 +40,8 @@ What differs from the reference, by design:
 from __future__ import annotations
 
 import warnings
+import weakref
+from collections import OrderedDict
 from dataclasses import dataclass
 from types import SimpleNamespace
 from typing import Dict, List, Optional, Sequence, Tuple
@@ -78,6 +80,10 @@ class ZOArguments:
     zo_fuse_next_perturb: bool = True
     # build-specific: replay each step as a captured hipGraph (ZOTrainer only)
     zo_graph: bool = False
+    # build-specific: compute logits only at the option positions the
+    # classification loss reads (HF's logits_to_keep) instead of at every
+    # position; the loss agrees with the full-logit one to rounding
+    zo_option_head: bool = False
 
 
 def layout_z_offsets(numels: Sequence[int]) -> List[int]:
@@ -108,21 +114,97 @@ def select_trainable(model: torch.nn.Module) -> Tuple[List[Tuple[str, torch.nn.P
     return named, exclude
 
 
+_HOST_INTS: "OrderedDict[int, tuple]" = OrderedDict()
+_HOST_INTS_MAX = 256
+
+
+def host_ints(x) -> List[int]:
+    """The integers of a small per-batch field (option_len, num_options) on the
+    host. A list or a CPU tensor is read directly; a device tensor is copied
+    back once and remembered by identity and version, so a batch that is used
+    for both forwards of a step (or again in later steps) costs one copy."""
+    if not torch.is_tensor(x):
+        return [int(v) for v in x]
+    if x.device.type == "cpu":
+        return [int(v) for v in x.tolist()]
+    try:
+        version = x._version
+    except RuntimeError:  # inference tensors carry no version counter
+        return [int(v) for v in x.tolist()]
+    hit = _HOST_INTS.get(id(x))
+    if hit is not None and hit[0]() is x and hit[1] == version:
+        return hit[2]
+    vals = [int(v) for v in x.tolist()]
+    _HOST_INTS[id(x)] = (weakref.ref(x), version, vals)
+    if len(_HOST_INTS) > _HOST_INTS_MAX:
+        _HOST_INTS.popitem(last=False)
+    return vals
+
+
+def option_window(option_len: Sequence[int], seq_len: int) -> Optional[int]:
+    """How many trailing positions of logits the option-masked loss reads:
+    max(option_len) + 1 (the logits at position j predict token j + 1). None
+    when that is the whole sequence, or when some option_len is 0: the
+    reference's ``shift_labels[i, :-0]`` is an empty slice, so such a row
+    keeps every position (trainer.py:1473-1475)."""
+    if len(option_len) == 0 or min(option_len) <= 0:
+        return None
+    k = max(option_len) + 1
+    return k if k < seq_len else None
+
+
+def shift_option_labels(input_ids: torch.Tensor, option_len, pad_id: int,
+                        window: Optional[int] = None) -> torch.Tensor:
+    """trainer.py:1469-1475: next-token targets, -100 at pad ids and at every
+    position before each row's last option_len tokens. Over all L - 1 shifted
+    positions, or over the last window - 1 of them when window is given.
+
+    The reference's per-row loop ``shift_labels[i, :-len] = -100`` is written as
+    one mask that sets the same elements: shifted position p is masked when
+    p < (L - 1) - len and len > 0 (the slice [:-0] is empty). masked_fill_
+    needs no device-to-host sync, so the loss can be captured in a graph."""
+    L = input_ids.shape[1]
+    first = 1 if window is None else L - window + 1  # first target position
+    labels = torch.clone(input_ids)[..., first:].contiguous()
+    labels.masked_fill_(labels == pad_id, -100)
+    if option_len is not None:
+        ol = torch.as_tensor(option_len, device=labels.device).reshape(-1, 1)
+        pos = torch.arange(first - 1, L - 1, device=labels.device).reshape(1, -1)
+        labels.masked_fill_((pos < (L - 1) - ol) & (ol > 0), -100)
+    return labels
+
+
 def option_len_loss(model, build_graph: bool, input_ids=None, labels=None, option_len=None, num_options=None,
-                    return_dict=None, **kwargs):
+                    return_dict=None, *, dz_window: Optional[int] = None, **kwargs):
     """The option-masked classification loss of trainer.py:1446-1522 (and of its
     copy in DiZO, trainer.py:470-542, which differs only by building the
     autograd graph: build_graph=True).
 
     Same torch operations in the same order, so the loss (in the model dtype)
-    is the reference's for the same logits. The per-example masking loop of
-    trainer.py:1473-1475 is written as one vectorised mask (positions before
-    the last option_len tokens), which sets the same elements. The forward
-    runs without a key/value cache (use_cache=False unless the caller says
-    otherwise): a loss never reads it, and building it costs two
-    concatenations per layer; the logits are the same.
+    is the reference's for the same logits. The forward runs without a
+    key/value cache (use_cache=False unless the caller says otherwise): a loss
+    never reads it, and building it costs two concatenations per layer; the
+    logits are the same.
+
+    Option head (``model.dz_option_head``, or an explicit ``dz_window``): the
+    classification branch reads the logits of the last max(option_len) + 1
+    positions only, so the forward asks HF for just those (logits_to_keep)
+    and the LM head, log_softmax and gather run over that window; the masked
+    positions outside it contribute nothing in the reference. The per-row
+    arithmetic is the same; the LM-head GEMM has fewer rows, so the logits,
+    and with them the loss, can differ from the full-logit ones by rounding.
+    With the option head and return_dict falsy the logits returned are the
+    window's. dz_window = 0 asks for the full logits without looking at
+    option_len (a captured graph decides the window on the host beforehand).
     """
     kwargs.setdefault("use_cache", False)
+    window = dz_window
+    if (window is None and labels is not None and option_len is not None and num_options is not None
+            and getattr(model, "dz_option_head", False)):
+        window = option_window(host_ints(option_len), input_ids.shape[1])
+    window = window or None
+    if window is not None:
+        kwargs["logits_to_keep"] = window
     if build_graph:
         outputs = model.forward(input_ids=input_ids, **kwargs)
     else:
@@ -132,14 +214,7 @@ def option_len_loss(model, build_graph: bool, input_ids=None, labels=None, optio
         return outputs
     logits = outputs.logits
     shift_logits = logits[..., :-1, :].contiguous()
-    shift_labels = torch.clone(input_ids)[..., 1:].contiguous()
-    # masked_fill_ sets the same elements as the reference's boolean-index
-    # assignments without a device-to-host sync (so the loss can be captured)
-    shift_labels.masked_fill_(shift_labels == model.config.pad_token_id, -100)
-    if option_len is not None:
-        ol = torch.as_tensor(option_len, device=shift_labels.device).reshape(-1, 1)
-        pos = torch.arange(shift_labels.shape[1], device=shift_labels.device).reshape(1, -1)
-        shift_labels.masked_fill_(pos < shift_labels.shape[1] - ol, -100)
+    shift_labels = shift_option_labels(input_ids, option_len, model.config.pad_token_id, window)
     loss_fct = CrossEntropyLoss(ignore_index=-100)
     if num_options is not None:
         log_probs = F.log_softmax(shift_logits, dim=-1)
@@ -147,8 +222,7 @@ def option_len_loss(model, build_graph: bool, input_ids=None, labels=None, optio
         shift_labels.masked_fill_(~mask, 0)
         selected = torch.gather(log_probs, dim=-1, index=shift_labels.unsqueeze(-1)).squeeze(-1)
         selected = (selected * mask).sum(-1) / mask.sum(-1)
-        # a host list of option counts avoids a sync; a tensor is read back
-        nopt = [int(x) for x in (num_options.tolist() if torch.is_tensor(num_options) else num_options)]
+        nopt = host_ints(num_options)
         if any(x != nopt[0] for x in nopt):
             loss, start, count = 0, 0, 0
             while start < len(nopt):
@@ -246,6 +320,7 @@ class ZOTrainerMixin:
         self._pending_restore = None  # (seed, eps): the +1 that ends zo_step
         self._pending_update = None   # (seed, eps, g, lr): restore + update of zo_update
         self.kernel_timer = None
+        model.dz_option_head = bool(getattr(args, "zo_option_head", False))
         self._hook = model.register_forward_pre_hook(lambda m, a: self.zo_flush())
 
     def _get_learning_rate(self) -> float:

@@ -2,7 +2,9 @@
 
 trainer.py:1446-1522 (forward_wrap_with_option_len), classification branch:
 for every row r (one candidate of one example), the option tokens are the
-last option_len[r] positions; each option token t at position j is predicted
+last option_len[r] positions (all positions when option_len[r] is 0: the
+reference masks with ``shift_labels[i, :-len]``, and [:-0] is an empty
+slice, trainer.py:1473-1475); each option token t at position j is predicted
 by the logits at position j - 1; pad ids (config.pad_token_id) are never
 targets. The row score is the mean over its option tokens of
 log_softmax(logits[j - 1])[t]. Rows are grouped into examples of
@@ -26,7 +28,8 @@ def row_scores(logits: np.ndarray, input_ids: np.ndarray, option_len: Sequence[i
     out = np.zeros(rows, dtype=np.float64)
     for r in range(rows):
         total, count = 0.0, 0
-        for j in range(L - int(option_len[r]), L):
+        ol = int(option_len[r])
+        for j in range(L - ol if ol > 0 else 1, L):
             if j < 1:
                 continue
             tok = int(input_ids[r, j])

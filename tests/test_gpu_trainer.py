@@ -265,11 +265,12 @@ def test_dizo_first_order_event_matches_reference(dt):
     dtr.close()
 
 
-def _run_trainer(dt, graph, enhanced, steps, batches, seed=31):
+def _run_trainer(dt, graph, enhanced, steps, batches, seed=31, option_head=False):
     from dizo_amd.synth import Cycle, build_opt
     from dizo_amd.trainer import ZOArguments, ZOTrainer
     model = build_opt("opt-tiny", dt, "cuda", seed=seed)
-    args = ZOArguments(learning_rate=1e-3, zo_eps=1e-3, max_steps=steps, enhanced=enhanced, zo_graph=graph)
+    args = ZOArguments(learning_rate=1e-3, zo_eps=1e-3, max_steps=steps, enhanced=enhanced, zo_graph=graph,
+                       zo_option_head=option_head)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches))
     it = iter(Cycle(batches))
@@ -302,4 +303,60 @@ def test_graph_steps_with_dizo_event_match_eager():
     le, pe = _run_trainer(torch.float16, False, "zo", 55, batches)
     lg, pg = _run_trainer(torch.float16, True, "zo", 55, batches)
     assert _same(le, lg)
+    assert all(_same(a, b) for a, b in zip(pe, pg))
+
+
+def _ulp(x: float, dt) -> float:
+    t = torch.tensor(abs(x), dtype=dt)
+    return float(torch.nextafter(t, torch.tensor(float("inf"), dtype=dt)).double() - t.double())
+
+
+def _option_batches():
+    from dizo_amd.synth import make_batches
+    padded = make_batches(2, 4, 512, seed=51, device="cuda", min_len=8, max_len=20)
+    fixed = make_batches(1, 4, 512, seed=52, device="cuda", fixed_len=24)
+    longer = make_batches(1, 3, 512, seed=53, device="cuda", min_len=10, max_len=14)
+    longer[0]["option_len"] = torch.tensor([2, 3, 1, 2, 3, 1], device="cuda")
+    return padded + fixed + longer
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_option_head_loss_matches_full_logits(dt):
+    """The option-position head (logits only for the last max(option_len) + 1
+    positions) against the full-logit loss on the device, same weights: the
+    LM-head GEMM has fewer rows, so the two may round differently; they agree
+    within 2 units in the last place of the model dtype (fp32: 1e-5
+    relative). Against the float64 brute force on the same logits the loss
+    carries the rounding of each log-probability to the model dtype: within 2
+    units in the last place of the largest row score (fp32: 1e-4 relative)."""
+    from dizo_amd.synth import PAD_ID, build_opt
+    from dizo_amd.trainer import option_len_loss
+    from oracle import loss as OL
+    model = build_opt("opt-mini", dt, "cuda", seed=9).eval()
+    for b in _option_batches():
+        with torch.inference_mode():
+            full = float(option_len_loss(model, False, **b, return_dict=True).loss)
+            model.dz_option_head = True
+            head = float(option_len_loss(model, False, **b, return_dict=True).loss)
+            model.dz_option_head = False
+            logits = model(input_ids=b["input_ids"], attention_mask=b["attention_mask"]).logits
+        want = OL.classification_loss(logits.double().cpu().numpy(), b["input_ids"].cpu().numpy(),
+                                      b["labels"].tolist(), b["option_len"].tolist(), b["num_options"].tolist(),
+                                      PAD_ID)
+        tol = 1e-5 * abs(full) if dt == torch.float32 else 2 * _ulp(full, dt)
+        assert abs(head - full) <= tol, f"{dt}: head {head} vs full {full}"
+        scores = OL.row_scores(logits.double().cpu().numpy(), b["input_ids"].cpu().numpy(), b["option_len"].tolist(),
+                               PAD_ID)
+        tol = 1e-4 * abs(want) if dt == torch.float32 else 2 * _ulp(float(np.abs(scores).max()), dt)
+        assert abs(head - want) <= tol, f"{dt}: head {head} vs float64 {want}"
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_graph_steps_with_option_head_match_eager(dt):
+    """With the option head, captured-graph steps give the eager steps' losses and
+    parameters bit for bit (windows of 2 and 4 positions, padded and unpadded)."""
+    batches = _option_batches()
+    le, pe = _run_trainer(dt, False, None, 10, batches, option_head=True)
+    lg, pg = _run_trainer(dt, True, None, 10, batches, option_head=True)
+    assert _same(le, lg), f"losses differ: {le} vs {lg}"
     assert all(_same(a, b) for a, b in zip(pe, pg))

@@ -65,18 +65,114 @@ def test_multichoice_branch_matches_bruteforce(tiny_model):
     assert float(got) == pytest.approx(want, rel=1e-5, abs=1e-6)
 
 
-def test_vectorised_option_mask_equals_reference_loop():
+def test_option_mask_equals_reference_loop():
+    """shift_option_labels sets exactly the elements of the reference's loop,
+    option_len 0 (nothing masked) and longer than the row included; with a
+    window, the loop leaves nothing unmasked before it and the window's
+    columns are the loop's last ones."""
+    from dizo_amd.trainer import option_window, shift_option_labels
+
     gen = torch.Generator().manual_seed(3)
-    for _ in range(20):
-        rows, L = 6, int(torch.randint(4, 30, (1,), generator=gen))
+    windows = 0
+    for it in range(60):
+        rows, L = 6, int(torch.randint(2, 30, (1,), generator=gen))
         ids = torch.randint(0, 6, (rows, L), generator=gen)
-        ol = torch.randint(1, L, (rows,), generator=gen)
+        hi = L + 2 if it % 3 == 0 else max(2, L // 3)
+        ol = torch.randint(0 if it % 4 == 0 else 1, hi, (rows,), generator=gen)
         want = _loop_mask(ids, ol, 1)
-        got = torch.clone(ids)[..., 1:].contiguous()
-        got[got == 1] = -100
-        pos = torch.arange(got.shape[1]).reshape(1, -1)
-        got[pos < got.shape[1] - ol.reshape(-1, 1)] = -100
-        assert torch.equal(got, want)
+        assert torch.equal(shift_option_labels(ids, ol, 1), want)
+        w = option_window(ol.tolist(), L)
+        if w is None:
+            assert int(ol.min()) == 0 or int(ol.max()) + 1 >= L
+            continue
+        windows += 1
+        assert bool((want[:, :L - w] == -100).all())
+        assert torch.equal(shift_option_labels(ids, ol, 1, window=w), want[:, L - w:])
+    assert windows >= 10
+
+
+def test_option_window_edges():
+    from dizo_amd.trainer import option_window
+
+    assert option_window([1, 1, 1], 128) == 2
+    assert option_window([1, 3, 2], 10) == 4
+    assert option_window([1, 0, 2], 10) is None  # [:-0] keeps the whole row
+    assert option_window([9], 10) is None         # the window is the whole sequence
+    assert option_window([], 10) is None
+
+
+@pytest.mark.parametrize("case", ["padded", "multichoice", "zero_len"])
+def test_option_head_loss_equals_full_loss(tiny_model, case):
+    """The option-position head (logits only for the last max(option_len) + 1
+    positions) gives the full-logit loss; in float64 the only difference is
+    the LM head's row count, so they agree to ~1e-12. The float64
+    brute-force oracle pins both."""
+    from dizo_amd.synth import PAD_ID, make_batch
+    from dizo_amd.trainer import option_len_loss
+
+    m64 = tiny_model.double()
+    try:
+        gen = torch.Generator().manual_seed(21)
+        if case == "padded":
+            b = make_batch(4, 512, gen=gen, min_len=5, max_len=14)
+            b["input_ids"][1, -4] = PAD_ID
+        else:
+            rows, L = 5, 16
+            ids = torch.randint(2, 512, (rows, L), generator=gen)
+            ids[1, :3] = PAD_ID
+            ol = [2, 3, 1, 2, 4] if case == "multichoice" else [2, 0, 1, 2, 1]
+            b = {"input_ids": ids, "attention_mask": (ids != PAD_ID).long(),
+                 "labels": torch.tensor([1, 1, 0, 0, 0]), "option_len": torch.tensor(ol),
+                 "num_options": torch.tensor([2, 2, 3, 3, 3])}
+        with torch.no_grad():
+            full = option_len_loss(m64, False, **b, return_dict=True).loss
+            m64.dz_option_head = True
+            head = option_len_loss(m64, False, **b, return_dict=True).loss
+            logits = m64(input_ids=b["input_ids"], attention_mask=b["attention_mask"]).logits
+        want = OL.classification_loss(logits.numpy(), b["input_ids"].numpy(), b["labels"].tolist(),
+                                      b["option_len"].tolist(), b["num_options"].tolist(), PAD_ID)
+        assert float(full) == pytest.approx(want, rel=1e-10, abs=1e-12)
+        assert float(head) == pytest.approx(float(full), rel=1e-10, abs=1e-12)
+    finally:
+        m64.dz_option_head = False
+        m64.float()
+
+
+def test_option_head_asks_for_the_window_only(tiny_model):
+    """With the option head the forward is asked for max(option_len) + 1
+    positions of logits, not the whole sequence."""
+    from dizo_amd.synth import make_batch
+    from dizo_amd.trainer import option_len_loss
+
+    b = make_batch(2, 512, gen=torch.Generator().manual_seed(5), min_len=20, max_len=24)
+    b["option_len"] = torch.tensor([1, 2, 1, 3])
+    seen = {}
+    orig = tiny_model.forward
+
+    def spy(*a, **kw):
+        seen.update(kw)
+        return orig(*a, **kw)
+
+    tiny_model.forward = spy
+    try:
+        tiny_model.dz_option_head = True
+        with torch.no_grad():
+            out = option_len_loss(tiny_model, False, **b)
+        assert seen["logits_to_keep"] == 4
+        assert out[1].shape[1] == 4
+    finally:
+        tiny_model.dz_option_head = False
+        del tiny_model.forward
+
+
+def test_host_ints_reads_a_tensor_once_per_version():
+    from dizo_amd.trainer import host_ints
+
+    t = torch.tensor([2, 2, 3])
+    assert host_ints(t) == [2, 2, 3]
+    assert host_ints([1, 2]) == [1, 2]
+    t[0] = 5
+    assert host_ints(t) == [5, 2, 3]
 
 
 def test_bruteforce_closed_forms():
