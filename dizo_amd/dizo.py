@@ -143,6 +143,8 @@ class DiZO(nn.Module):
         self._fo_tab: Optional[ProjTable] = None
         self._fo_params: Optional[List[torch.Tensor]] = None
         self._fo_dirty = False
+        # optional record of every pass that changes theta (checkpoint.ZOJournal)
+        self.journal = None
 
     # ---------------------------------------------------------- gamma ----
     @property
@@ -207,6 +209,8 @@ class DiZO(nn.Module):
         else:
             raise DzError(f"DiZO: alpha is {alpha.dtype} but the projected tensors are {tab.dtype}")
         self._timed("proj_apply", tab, 3, lambda: tab.project(alpha, mode))
+        if self.journal is not None:
+            self.journal.proj("apply" if mode == L.DZ_PROJ_APPLY else "apply_f32", alpha)
         self._alpha_vec = alpha
         self._norms = None
         self.alpha = {name: alpha[i:i + 1] for i, name in enumerate(self.constraints_name)}
@@ -221,6 +225,8 @@ class DiZO(nn.Module):
         norms = torch.empty(self.G, dtype=tab.dtype, device=tab.device)
         self._timed("proj_reverse_sumsq", tab, 3,
                     lambda: tab.project(self._alpha_vec, L.DZ_PROJ_REVERSE_SUMSQ, norm_T=norms))
+        if self.journal is not None:
+            self.journal.proj("reverse", self._alpha_vec)
         self._norms = norms
         return norms
 
@@ -323,6 +329,8 @@ class DiZO(nn.Module):
             for b, p in zip(self._fo_saved, ps):
                 b.copy_(p.data)
         self._fo_params = ps
+        if self.journal is not None:
+            self.journal.mark()
         return ps
 
     def fo_restore(self) -> None:
@@ -336,6 +344,8 @@ class DiZO(nn.Module):
                     p.data.copy_(b)
             self._fo_dirty = False
             self._norms = None
+            if self.journal is not None:
+                self.journal.rollback()
 
     def forward(self, new=None, pre_trained=None, x=None, apply=False):
         """trainer.py:714-741: with apply, the final projection; otherwise the
@@ -380,20 +390,36 @@ class dizo_trainer:  # noqa: N801 (reference name)
         self.criterion = torch.nn.CrossEntropyLoss()
         self.i = 0
         self.gamma_seed = 0
+        self.batches_drawn = 0  # gamma-search batches taken so far (for checkpoints)
 
     def bind_model(self, model) -> None:
         """Registers the projection table of (model, anchor) ahead of the first event."""
         self.dizo._table(model, self.pre_trained)
 
-    def _next_batch(self):
-        if self.pgmloader is None:
-            raise DzError("dizo_trainer: no data loader for the gamma search")
+    def _draw(self):
         try:
             data = next(self.dataset_iterator)
         except StopIteration:
             self.dataset_iterator = iter(self.pgmloader)
             data = next(self.dataset_iterator)
+        self.batches_drawn += 1
+        return data
+
+    def _next_batch(self):
+        if self.pgmloader is None:
+            raise DzError("dizo_trainer: no data loader for the gamma search")
+        data = self._draw()
         return {k: (v.to(self.device) if torch.is_tensor(v) else v) for k, v in data.items()}
+
+    def rewind_loader(self, drawn: int) -> None:
+        """Restarts the gamma search's loader and skips the `drawn` batches a
+        checkpointed run had taken (exact for a loader with a fixed order)."""
+        self.batches_drawn = 0
+        if self.pgmloader is None:
+            return
+        self.dataset_iterator = iter(self.pgmloader)
+        for _ in range(drawn):
+            self._draw()
 
     def dizo_zo_iters(self, model, base_model, apply=False):
         """trainer.py:782-803: max_iters SPSA iterations on gamma, then the final apply."""

@@ -84,6 +84,10 @@ class ZOArguments:
     # classification loss reads (HF's logits_to_keep) instead of at every
     # position; the loss agrees with the full-logit one to rounding
     zo_option_head: bool = False
+    # build-specific: keep a journal of every pass that changes the trainable
+    # tensors (seed, g, lr per step; DiZO projections), for exact replay and
+    # checkpoints (dizo_amd.checkpoint)
+    zo_journal: bool = False
 
 
 def layout_z_offsets(numels: Sequence[int]) -> List[int]:
@@ -321,6 +325,14 @@ class ZOTrainerMixin:
         self._pending_update = None   # (seed, eps, g, lr): restore + update of zo_update
         self.kernel_timer = None
         model.dz_option_head = bool(getattr(args, "zo_option_head", False))
+        self.zo_journal = None
+        if getattr(args, "zo_journal", False):
+            from .checkpoint import ZOJournal
+
+            projected = self.dizo_trainer.dizo.constraints_name if args.enhanced else []
+            self.zo_journal = ZOJournal.for_params(self.named_parameters_to_optim, args.zo_eps, projected)
+            if args.enhanced:
+                self.dizo_trainer.dizo.journal = self.zo_journal
         self._hook = model.register_forward_pre_hook(lambda m, a: self.zo_flush())
 
     def _get_learning_rate(self) -> float:
@@ -437,6 +449,8 @@ class ZOTrainerMixin:
         else:
             self.zo_flush()
             self._launch("update", lambda t: t.update(seed, g, lr), tabs)
+        if self.zo_journal is not None:
+            self.zo_journal.zo(seed, g, lr)
         if event_due:
             self.dizo_trainer.gamma_seed = seed
             if args.enhanced == "zo":
@@ -541,6 +555,8 @@ class ZOTrainer(ZOTrainerMixin):
         lr = self._get_learning_rate()
         tr_loss_step = self._graph.step(inputs, self.zo_random_seed, lr).clone()
         self.projected_grad = None
+        if self.zo_journal is not None:
+            self.zo_journal.zo(self.zo_random_seed, self._graph.d_prev_g.clone(), lr)
         self._account(tr_loss_step)
         if (self.state.global_step + 1) % DIZO_INTERVAL == 0 and args.enhanced:
             self.zo_flush()
