@@ -29,6 +29,51 @@ def zo_update(params: Sequence[torch.Tensor], zs: Sequence[torch.Tensor], projec
         param.data = param.data - lr * (projected_grad * z)
 
 
+def _f32(x: float) -> float:
+    """A Python scalar as torch's kernels use it with a 16-bit or fp32 tensor:
+    converted to the fp32 "opmath" type."""
+    return float(torch.tensor(x, dtype=torch.float32))
+
+
+def _rt(x64: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """An exactly computed float64 value rounded as torch's CPU and CUDA kernels
+    round an fp32-opmath result: to fp32 (the op), then to the tensor dtype."""
+    return x64.float().to(dtype)
+
+
+def zo_perturb_parameters_recipe(params: Sequence[torch.Tensor], zs: Sequence[torch.Tensor],
+                                 scaling_factor: float, zo_eps: float) -> None:
+    """trainer.py:1438-1442 with z supplied, each operation evaluated exactly in
+    float64 and rounded as torch's CPU and CUDA kernels round it (fp32 result,
+    then the parameter dtype): R(p + R(R(s * z) * eps)).
+
+    Products of a 16-bit (or fp32) value and an fp32 scalar are exact in
+    float64, so this is the recipe itself on any device. It exists for device
+    runs: on some launch paths (seen on tensors of 1 and 2,560 elements, not
+    on 1M) ROCm torch's 16-bit `scalar * tensor` kernel rounds the exact
+    product to the 16-bit type once, which differs from the recipe when the
+    fp32 product falls exactly halfway between two 16-bit values (a rare tie;
+    torch on the CPU and CUDA rounds the tie to even from the fp32 product)."""
+    s, eps = _f32(scaling_factor), _f32(zo_eps)
+    for param, z in zip(params, zs):
+        dt = param.dtype
+        a = _rt(z.double() * s, dt)
+        b = _rt(a.double() * eps, dt)
+        param.data = _rt(param.data.double() + b.double(), dt)
+
+
+def zo_update_recipe(params: Sequence[torch.Tensor], zs: Sequence[torch.Tensor], projected_grad: float,
+                     lr: float) -> None:
+    """trainer.py:1603-1608 with z supplied, in the recipe form of
+    zo_perturb_parameters_recipe: R(p - R(lr * R(g * z)))."""
+    g, lr32 = _f32(projected_grad), _f32(lr)
+    for param, z in zip(params, zs):
+        dt = param.dtype
+        c = _rt(z.double() * g, dt)
+        d = _rt(c.double() * lr32, dt)
+        param.data = _rt(param.data.double() - d.double(), dt)
+
+
 def zo_perturb_parameters_sampled(params: Sequence[torch.Tensor], seed: int, scaling_factor: float,
                                   zo_eps: float) -> None:
     """trainer.py:1438-1442 verbatim, z drawn by torch.normal (the CPU-baseline workload)."""

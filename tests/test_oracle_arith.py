@@ -215,3 +215,62 @@ def test_gamma_iteration_matches_torch(dt):
     for g in range(G):
         assert_bits_equal(gam[g:g + 1], to_bits(gammas[g].reshape(1)), dt, f"gamma {g}")
         assert_bits_equal(th2[g], to_bits(news[g]), dt, f"theta {g}")
+
+
+def _tie_cases(dt, n_want=64, seed=5):
+    """(value, fp32 scalar) pairs whose fp32 product lies exactly halfway between
+    two neighbours in dt while the exact product does not: rounding the exact
+    product once and rounding the fp32 product (to even) can differ."""
+    g = np.random.default_rng(seed)
+    out = []
+    while len(out) < n_want:
+        v = torch.tensor(g.standard_normal(1 << 16) * 40, dtype=torch.float32).to(dt)
+        s = float(np.float32(g.uniform(1e-7, 2e-6)))
+        exact = v.double() * s
+        p32 = exact.float()
+        lo = p32.to(dt)
+        away = torch.where(p32 > lo.float(), torch.tensor(np.inf), torch.tensor(-np.inf)).to(dt)
+        nxt = torch.nextafter(lo, away)
+        mid = (lo.double() + nxt.double()) / 2
+        hit = (p32.double() == mid) & (exact != p32.double()) & (lo != nxt) & torch.isfinite(nxt.float())
+        for i in hit.nonzero().flatten().tolist()[:8]:
+            out.append((float(v[i]), s))
+    return out
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_recipe_reference_equals_torch_cpu_on_ties(dt):
+    """oracle.ref_torch's recipe form (exact float64 products rounded to fp32,
+    then to dt) gives torch's CPU kernels bit for bit on products whose fp32
+    value is an exact tie in dt, where a single rounding of the exact product
+    would differ; among them the update seen at OPT-2.7B scale, lr 9.15e-07
+    times -33.90625 (a tie at -520.5 fp16 subnormal units)."""
+    cases = _tie_cases(dt)
+    if dt == torch.float16:
+        cases.append((-33.90625, float(np.float32(9.15e-07))))
+    c = torch.tensor([v for v, _ in cases], dtype=torch.float32).to(dt)
+    for i, (v, s) in enumerate(cases):
+        x = c[i:i + 1].clone()
+        want = s * x                                     # torch's CPU kernel
+        got = R._rt(x.double() * R._f32(s), dt)          # recipe
+        assert torch.equal(want.view(torch.int16), got.view(torch.int16)), (v, s, float(want), float(got))
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
+def test_recipe_step_equals_torch_cpu(dt):
+    """The recipe forms of the perturbation and the update equal the reference's
+    expressions on torch's CPU kernels (random weights and z, several scales)."""
+    g = torch.Generator().manual_seed(3)
+    p = (torch.randn(50000, generator=g) * 0.02).to(dt)
+    z = torch.randn(50000, generator=g).to(dt)
+    for s, eps, gr, lr in ((1, 1e-3, 0.75, 1e-6), (-2, 1e-3, -51.03125, 9.15e-07), (1, 3e-4, 2.5, 1e-3)):
+        a, b = [p.clone()], [p.clone()]
+        R.zo_perturb_parameters(a, [z], s, eps)
+        R.zo_perturb_parameters_recipe(b, [z], s, eps)
+        assert torch.equal(a[0].view(BITS[dt]), b[0].view(BITS[dt]))
+        R.zo_update(a, [z], gr, lr)
+        R.zo_update_recipe(b, [z], gr, lr)
+        assert torch.equal(a[0].view(BITS[dt]), b[0].view(BITS[dt]))
+
+
+BITS = {torch.float32: torch.int32, torch.float16: torch.int16, torch.bfloat16: torch.int16}
