@@ -253,6 +253,62 @@ class DiZO(nn.Module):
         self._freeze(new)
         self._reverse(tab)
 
+    # ------------------------------------------- supplied / searched -----
+    def apply_ratio(self, new, pre_trained, alpha) -> None:
+        """theta <- theta0 + alpha (theta - theta0) for every projected tensor with a
+        supplied ratio (one number for all groups, or one per group; the "alpha
+        supplied" form, e.g. a fixed 0.9 per layer). alpha is rounded to the model
+        dtype and applied as trainer.py:428-436 applies gamma / (norm + 1e-8)."""
+        tab = self._table(new, pre_trained)
+        a = torch.as_tensor(alpha, dtype=torch.float64).reshape(-1)
+        if a.numel() == 1:
+            a = a.expand(self.G)
+        if a.numel() != self.G:
+            raise DzError(f"DiZO.apply_ratio: {a.numel()} ratios for {self.G} groups")
+        self._freeze(new)
+        self._apply_alpha(tab, a.float().to(tab.dtype).to(tab.device).contiguous())
+
+    def apply_gamma(self, new, pre_trained, gamma) -> None:
+        """apply_constraints with supplied gamma (target norms ||theta - theta0||;
+        one number for all groups, or one per group; the "gamma supplied" form).
+        A Python number or list is an fp32 gamma, as the reference's constraint
+        Parameters are (alpha is then fp32 and the result is rounded once); a
+        tensor keeps its dtype."""
+        if torch.is_tensor(gamma):
+            g = gamma.detach().reshape(-1).to(self._device)
+        else:
+            g = torch.as_tensor(gamma, dtype=torch.float32, device=self._device).reshape(-1)
+        if g.numel() == 1:
+            g = g.expand(self.G)
+        if g.numel() != self.G:
+            raise DzError(f"DiZO.apply_gamma: {g.numel()} values for {self.G} groups")
+        self._set_gamma(g.clone())
+        self.apply_constraints(new, pre_trained, iter(self.constraints))
+
+    def grid_search(self, new, pre_trained, x, candidates: Sequence[float]):
+        """Searched ratio: the loss on batch x at each candidate ratio (the same for
+        every group, e.g. 8 values in [0.5, 1.0]), each evaluated from the same
+        theta (the projected tensors are restored exactly between candidates),
+        then the candidate with the lowest loss (the first of equals) applied.
+        Returns (chosen ratio, losses)."""
+        if len(candidates) == 0:
+            raise DzError("DiZO.grid_search: no candidates")
+        self.fo_restore()
+        self._fo_snapshot(new, pre_trained)
+        losses = []
+        with torch.no_grad():
+            for r in candidates:
+                if self.journal is not None:
+                    self.journal.mark()  # the candidate's apply is undone below
+                self.apply_ratio(new, pre_trained, r)
+                self._fo_dirty = True
+                losses.append(self._loss(new, x).reshape(()).float())
+                self.fo_restore()
+            best = int(torch.stack(losses).argmin().item())
+            self.apply_ratio(new, pre_trained, candidates[best])
+        self.last_losses = tuple(losses)
+        return float(candidates[best]), losses
+
     def _project_ratio(self, new, anchor, constraint_iterator):
         """trainer.py:453-465 for one projected tensor `new` with anchor `anchor`."""
         if self._tab is None:
@@ -442,6 +498,14 @@ class dizo_trainer:  # noqa: N801 (reference name)
             dz._in_event = False
             dz._norms = None
         self.i += 1
+
+    def dizo_grid_iters(self, model, base_model, candidates: Sequence[float]) -> float:
+        """The searched-ratio event: one batch from the loader, the loss at each
+        candidate ratio, the best one applied (DiZO.grid_search). Returns the ratio."""
+        data = self._next_batch()
+        r, _ = self.dizo.grid_search(model, base_model, data, candidates)
+        self.i += 1
+        return r
 
     def dizo_iters(self, model, base_model, apply=False):
         """trainer.py:805-830: max_iters first-order iterations (Adam on gamma,

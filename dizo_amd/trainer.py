@@ -67,7 +67,7 @@ class ZOArguments:
     learning_rate: float = 1e-7
     zo_eps: float = 1e-3
     max_steps: int = 20000
-    enhanced: Optional[str] = None  # None | "zo" | "fo" (dizo.sh passes the string "None")
+    enhanced: Optional[str] = None  # None | "zo" | "fo" (dizo.sh passes the string "None"); build: "grid"
     gradient_accumulation_steps: int = 1
     non_diff: bool = False
     n_gpu: int = 1
@@ -88,6 +88,9 @@ class ZOArguments:
     # tensors (seed, g, lr per step; DiZO projections), for exact replay and
     # checkpoints (dizo_amd.checkpoint)
     zo_journal: bool = False
+    # build-specific: ratios tried by ENHANCED=grid (the searched-ratio DiZO
+    # event: loss at each ratio, best applied); None = 8 values in [0.5, 1.0]
+    dizo_grid: Optional[Tuple[float, ...]] = None
 
 
 def layout_z_offsets(numels: Sequence[int]) -> List[int]:
@@ -308,7 +311,7 @@ class ZOTrainerMixin:
         self.lr_scheduler = torch.optim.lr_scheduler.LambdaLR(
             optimizer, lambda step: 1 - self.state.global_step / (2 * args.max_steps))
         self.named_parameters_to_optim, self.exclude_list = select_trainable(model)
-        if args.enhanced in ("zo", "fo"):
+        if args.enhanced in ("zo", "fo", "grid"):
             if base_model is None:
                 base_model = _anchor_copy(model, self.exclude_list)
             self.base_model = base_model
@@ -452,12 +455,21 @@ class ZOTrainerMixin:
         if self.zo_journal is not None:
             self.zo_journal.zo(seed, g, lr)
         if event_due:
-            self.dizo_trainer.gamma_seed = seed
-            if args.enhanced == "zo":
-                self.dizo_trainer.dizo_zo_iters(model, base_model=self.base_model)
-            else:
-                self.dizo_trainer.dizo_iters(model, base_model=self.base_model)
+            self._dizo_event(model, seed)
         self.lr_scheduler.step()
+
+    def _dizo_event(self, model, seed: int) -> None:
+        """The DiZO event of trainer.py:1611-1615 (after the update of every 50th step)."""
+        args = self.args
+        self.zo_flush()
+        self.dizo_trainer.gamma_seed = seed
+        if args.enhanced == "zo":
+            self.dizo_trainer.dizo_zo_iters(model, base_model=self.base_model)
+        elif args.enhanced == "fo":
+            self.dizo_trainer.dizo_iters(model, base_model=self.base_model)
+        else:
+            grid = args.dizo_grid if args.dizo_grid is not None else tuple(np.linspace(0.5, 1.0, 8))
+            self.dizo_trainer.dizo_grid_iters(model, self.base_model, grid)
 
     def export_z(self, name: str, seed: Optional[int] = None) -> torch.Tensor:
         """The z that seed (default: the current zo_random_seed) applies to
@@ -559,12 +571,7 @@ class ZOTrainer(ZOTrainerMixin):
             self.zo_journal.zo(self.zo_random_seed, self._graph.d_prev_g.clone(), lr)
         self._account(tr_loss_step)
         if (self.state.global_step + 1) % DIZO_INTERVAL == 0 and args.enhanced:
-            self.zo_flush()
-            self.dizo_trainer.gamma_seed = self.zo_random_seed
-            if args.enhanced == "zo":
-                self.dizo_trainer.dizo_zo_iters(self.model, base_model=self.base_model)
-            else:
-                self.dizo_trainer.dizo_iters(self.model, base_model=self.base_model)
+            self._dizo_event(self.model, self.zo_random_seed)
         self.lr_scheduler.step()
         self._finish_step(tr_loss_step)
         return tr_loss_step

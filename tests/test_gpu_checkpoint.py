@@ -47,7 +47,7 @@ def _run(tr, it, n):
 @pytest.mark.parametrize("dt,enhanced,graph", [
     (torch.float16, None, False), (torch.bfloat16, None, False), (torch.float32, None, False),
     (torch.float16, "zo", False), (torch.bfloat16, "zo", False), (torch.float16, "fo", False),
-    (torch.float16, "zo", True), (torch.bfloat16, None, True),
+    (torch.float16, "zo", True), (torch.bfloat16, None, True), (torch.float16, "grid", False),
 ])
 def test_replay_reproduces_the_run(dt, enhanced, graph, tmp_path):
     """55 steps (a DiZO event at global step 49 when enhanced): replaying the
@@ -69,7 +69,7 @@ def test_replay_reproduces_the_run(dt, enhanced, graph, tmp_path):
     journal = ZOJournal.load(path)
     assert journal.steps == 55
     n_proj = sum(1 for op in journal.ops if op[0] != "zo")
-    assert n_proj == {None: 0, "zo": 41, "fo": 1}[enhanced]
+    assert n_proj == {None: 0, "zo": 41, "fo": 1, "grid": 1}[enhanced]
 
     fresh, anchor = copy.deepcopy(init), copy.deepcopy(init)
     assert replay(fresh, journal, base_model=anchor) == 55
