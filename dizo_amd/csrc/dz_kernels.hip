@@ -167,8 +167,12 @@ __device__ __forceinline__ uint32_t table_entry(uint32_t qbits, const DzScalars&
 }
 
 typedef _Float16 dz_half2 __attribute__((ext_vector_type(2)));
+typedef __bf16 dz_bf2 __attribute__((ext_vector_type(2)));
 
-// R_T(a + b) for a pair of 16-bit values packed in one word.
+// R_T(a + b) for a pair of 16-bit values packed in one word: fp16 adds
+// natively (v_pk_add_f16); bf16 adds in fp32 and rounds both lanes with one
+// v_cvt_pk_bf16_f32 (RNE). Either equals the reference's fp32 add rounded
+// to T: fp32 holds at least 2p + 2 bits of a p-bit format.
 template <int DT>
 __device__ __forceinline__ uint32_t add_pair(uint32_t a, uint32_t b) {
   if constexpr (DT == DZ_F16) {
@@ -176,10 +180,19 @@ __device__ __forceinline__ uint32_t add_pair(uint32_t a, uint32_t b) {
     const dz_half2 y = __builtin_bit_cast(dz_half2, b);
     return __builtin_bit_cast(uint32_t, x + y);
   } else {
-    const float a0 = __uint_as_float(a << 16), a1 = __uint_as_float(a & 0xffff0000u);
-    const float b0 = __uint_as_float(b << 16), b1 = __uint_as_float(b & 0xffff0000u);
-    return DT_<DT>::from_f(a0 + b0) | (DT_<DT>::from_f(a1 + b1) << 16);
+    const dz_bf2 x = __builtin_bit_cast(dz_bf2, a);
+    const dz_bf2 y = __builtin_bit_cast(dz_bf2, b);
+    return __builtin_bit_cast(uint32_t, x + y);
   }
+}
+
+// Low (pack_lo) or high (pack_hi) 16-bit halves of two words, a's in the low
+// lane and b's in the high lane: one v_perm_b32.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
 // R_T(a + b) for one 16-bit value.
@@ -195,25 +208,25 @@ __device__ __forceinline__ uint32_t add_one(uint32_t a, uint32_t b) {
 
 // Two 16-bit elements (packed in `th`) whose z fields are the halves of `w`
 // (and, for the step-fused mode, whose next-step z fields are the halves of w2).
+// A field's sign bit (bit 15 of its half) negates its table value; once the
+// two lanes' values are packed, that is one xor with w & 0x80008000.
 template <int DT, int MODE>
 __device__ __forceinline__ uint32_t apply_pair16(uint32_t th, uint32_t w, uint32_t w2,
                                                  const typename RmwTraits<DT, MODE>::E* tab) {
+  const uint32_t sw = w & 0x80008000u;
   if constexpr (!rmw_pair_mode(MODE)) {
-    const uint32_t lo = (uint32_t)tab[w & 0x7fffu] ^ (w & 0x8000u);
-    const uint32_t hi = (uint32_t)tab[(w >> 16) & 0x7fffu] ^ ((w >> 16) & 0x8000u);
-    return add_pair<DT>(th, lo | (hi << 16));
+    const uint32_t t0 = tab[w & 0x7fffu], t1 = tab[(w >> 16) & 0x7fffu];
+    return add_pair<DT>(th, (t0 | (t1 << 16)) ^ sw);
   } else {
-    // entry = b | (-d) << 16; a negative z negates both halves
-    const uint32_t e0 = tab[w & 0x7fffu] ^ ((w & 0x8000u) * 0x10001u);
-    const uint32_t e1 = tab[(w >> 16) & 0x7fffu] ^ (((w >> 16) & 0x8000u) * 0x10001u);
-    const uint32_t b = (e0 & 0xffffu) | (e1 << 16);
-    const uint32_t nd = (e0 >> 16) | (e1 & 0xffff0000u);
+    // entry = b | (-d) << 16 for a positive z
+    const uint32_t e0 = tab[w & 0x7fffu], e1 = tab[(w >> 16) & 0x7fffu];
+    const uint32_t b = pack_lo(e0, e1) ^ sw;
+    const uint32_t nd = pack_hi(e0, e1) ^ sw;
     uint32_t r = add_pair<DT>(add_pair<DT>(th, b), nd);
     if constexpr (MODE == kModeRestoreUpdatePerturb) {
       // the next step's +1 perturbation uses the same b (same scale and eps)
-      const uint32_t f0 = (tab[w2 & 0x7fffu] ^ (w2 & 0x8000u)) & 0xffffu;
-      const uint32_t f1 = (tab[(w2 >> 16) & 0x7fffu] ^ ((w2 >> 16) & 0x8000u)) & 0xffffu;
-      r = add_pair<DT>(r, f0 | (f1 << 16));
+      const uint32_t f0 = tab[w2 & 0x7fffu], f1 = tab[(w2 >> 16) & 0x7fffu];
+      r = add_pair<DT>(r, pack_lo(f0, f1) ^ (w2 & 0x80008000u));
     }
     return r;
   }
