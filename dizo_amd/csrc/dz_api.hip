@@ -237,11 +237,11 @@ int32_t check_group_outputs(const dz_table* t, const double* d_sumsq, const floa
   return rc;
 }
 
-// Persistent grid of an RMW launch: as many 1024-thread workgroups as fit on
-// the device at once given the LDS delta table (64 KB: two per CU; 128 KB:
-// one per CU), but no more than there are tiles.
+// Persistent grid of an RMW launch: DZ_RMW_NARROW_WG_PER_CU 1024-thread
+// workgroups per CU for a 64 KB delta table, one for a 128 KB table, but no
+// more than there are tiles.
 uint32_t rmw_grid(const dz_table* t, int mode, uint32_t ntiles) {
-  const uint32_t per_cu = dz::rmw_lds_table_bytes(t->dtype, mode) <= 65536 ? 2u : 1u;
+  const uint32_t per_cu = dz::rmw_lds_table_bytes(t->dtype, mode) <= 65536 ? (uint32_t)DZ_RMW_NARROW_WG_PER_CU : 1u;
   const uint32_t g = per_cu * (uint32_t)t->dev->cus;
   return ntiles < g ? ntiles : g;
 }

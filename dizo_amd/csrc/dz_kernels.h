@@ -33,12 +33,13 @@ struct DzPtrArray {
 // Read-modify-write kernel geometry. A workgroup of 1024 threads takes one
 // tile (chunk) at a time from the table's work counters; each thread owns
 // rmw_groups(dtype, mode) groups of 8 elements per tile. Measured on the
-// MI355X at OPT-13B size: launches whose LDS table is 64 KB (two workgroups
-// per CU) stream best with 16 KB tiles (one group per thread, 6.1 TB/s);
-// launches with a 128 KB table (one workgroup per CU) with 64 KB tiles
-// (6.2 TB/s for restore+update). The macros let experiments build others.
+// MI355X at OPT-13B size (643 tensors, fp16): 64 KB tiles (four groups per
+// thread) and one workgroup per CU stream best for every mode: perturb 6.4
+// TB/s against 6.05 with 16 KB tiles and two workgroups per CU (which a 64 KB
+// table would allow), restore+update 6.4-6.5 TB/s. fp32 uses 64 KB tiles too
+// (two groups of 8 fp32 per thread). The macros let experiments build others.
 #ifndef DZ_RMW_GROUPS_NARROW
-#define DZ_RMW_GROUPS_NARROW 1
+#define DZ_RMW_GROUPS_NARROW 4
 #endif
 #ifndef DZ_RMW_GROUPS_WIDE16
 #define DZ_RMW_GROUPS_WIDE16 4
@@ -48,6 +49,14 @@ struct DzPtrArray {
 #endif
 #ifndef DZ_RMW_COUNTERS
 #define DZ_RMW_COUNTERS 8
+#endif
+// Workgroups per CU for launches with a 64 KB table (the LDS would allow two),
+// and next-tile prefetch for those launches (measured neutral).
+#ifndef DZ_RMW_NARROW_WG_PER_CU
+#define DZ_RMW_NARROW_WG_PER_CU 1
+#endif
+#ifndef DZ_RMW_PREFETCH_NARROW
+#define DZ_RMW_PREFETCH_NARROW 0
 #endif
 constexpr int kRmwThreads = 1024;
 __host__ __device__ constexpr int rmw_groups(int dtype, int mode) {

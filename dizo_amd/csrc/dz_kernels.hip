@@ -139,13 +139,13 @@ struct RmwTraits {
   using E = typename std::conditional<kWide, uint32_t, uint16_t>::type;
   static constexpr int kGroups = rmw_groups(DT, MODE);
   static constexpr int kChunk = rmw_chunk_elems(DT, MODE);
-  // Waves per SIMD when the LDS table lets two workgroups share a CU (the
-  // register budget then is 64 VGPRs), else one workgroup (4 waves).
-  static constexpr int kWavesPerEU = kWide ? 4 : 8;
+  // Waves per SIMD: 4 with one workgroup per CU (128 VGPRs per lane), 8 when
+  // two workgroups share a CU (64 VGPRs).
+  static constexpr int kWavesPerEU = (kWide || DZ_RMW_NARROW_WG_PER_CU == 1) ? 4 : 8;
   // Load tile k+1 while tile k computes: pays off for the two-seed pass, whose
   // ALU time (two Philox chains per group) is the largest; measured neutral to
   // negative for the others.
-  static constexpr bool kPrefetch = MODE == kModeRestoreUpdatePerturb;
+  static constexpr bool kPrefetch = MODE == kModeRestoreUpdatePerturb || (!kWide && DZ_RMW_PREFETCH_NARROW);
 };
 
 // Table entry for z = +Q_T[i] (qbits = bits of Q_T[i]).
