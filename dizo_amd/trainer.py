@@ -211,7 +211,13 @@ def option_len_loss(model, build_graph: bool, input_ids=None, labels=None, optio
         window = option_window(host_ints(option_len), input_ids.shape[1])
     window = window or None
     if window is not None:
-        kwargs["logits_to_keep"] = window
+        # as index positions, not a count: HF then gathers the window's hidden
+        # states into a contiguous tensor; the strided slice a count gives
+        # sends the LM-head GEMM to a ~20x slower kernel once the weights stop
+        # requiring grad (the DiZO projection clears requires_grad on every
+        # parameter, trainer.py:417)
+        L = input_ids.shape[1]
+        kwargs["logits_to_keep"] = torch.arange(L - window, L, device=input_ids.device)
     if build_graph:
         outputs = model.forward(input_ids=input_ids, **kwargs)
     else:

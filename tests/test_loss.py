@@ -139,8 +139,8 @@ def test_option_head_loss_equals_full_loss(tiny_model, case):
 
 
 def test_option_head_asks_for_the_window_only(tiny_model):
-    """With the option head the forward is asked for max(option_len) + 1
-    positions of logits, not the whole sequence."""
+    """With the option head the forward is asked for the logits of the last
+    max(option_len) + 1 positions (as index positions), not the whole sequence."""
     from dizo_amd.synth import make_batch
     from dizo_amd.trainer import option_len_loss
 
@@ -158,7 +158,8 @@ def test_option_head_asks_for_the_window_only(tiny_model):
         tiny_model.dz_option_head = True
         with torch.no_grad():
             out = option_len_loss(tiny_model, False, **b)
-        assert seen["logits_to_keep"] == 4
+        L = b["input_ids"].shape[1]
+        assert torch.equal(seen["logits_to_keep"], torch.arange(L - 4, L))
         assert out[1].shape[1] == 4
     finally:
         tiny_model.dz_option_head = False
