@@ -222,6 +222,43 @@ def kernel_microbench(wl_name: str, reps: int = 10, log=print):
         out[name] = {"ms": t, "GBps": nbytes / t / 1e6, "frac": nbytes / t / 1e6 / HBM_PEAK_GBPS}
         log(f"[kernels] {name:15s} {t:8.3f} ms {nbytes / t / 1e6:8.1f} GB/s")
     tabs.close()
+    # projection passes over the projected (k/v) tensors, theta0 a perturbed copy
+    from dizo_amd import _lib as L
+    from dizo_amd.dizo import DiZO
+    from dizo_amd.table import ProjTable
+
+    _, exclude = select_trainable(model)
+    names = DiZO(model, "l2norm", exclude).constraints_name
+    params = dict(model.named_parameters())
+    th = [params[n].data for n in names]
+    t0 = [(t.float() + 1e-3).to(t.dtype) for t in th]
+    ptab = ProjTable(th, t0)
+    G = len(names)
+    alpha = torch.full((G,), 0.9, dtype=dtype, device="cuda")
+    norms = torch.empty(G, dtype=dtype, device="cuda")
+    pbytes = ptab.bytes_per_tensor_pass
+    proj_cases = {
+        "proj_sumsq": (2, lambda: ptab.group_sumsq(norm_T=norms)),
+        "proj_apply": (3, lambda: ptab.project(alpha, L.DZ_PROJ_APPLY)),
+        "proj_reverse_sumsq": (3, lambda: ptab.project(alpha, L.DZ_PROJ_REVERSE_SUMSQ, norm_T=norms)),
+    }
+    for name, (k, fn) in proj_cases.items():
+        fn()
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ms.append(e0.elapsed_time(e1))
+        t = float(np.median(ms))
+        nb = k * pbytes
+        out[name] = {"ms": t, "GBps": nb / t / 1e6, "frac": nb / t / 1e6 / HBM_PEAK_GBPS, "bytes": nb}
+        log(f"[kernels] {name:15s} {t:8.3f} ms {nb / t / 1e6:8.1f} GB/s")
+    ptab.close()
+    del t0
     # calibration for counter-based traffic: a plain device copy of known size
     # (reads and writes copy_bytes each), launched twice
     copy_bytes = 4 << 30
@@ -307,6 +344,11 @@ def main(argv=None):
             "algorithmic_bytes_per_launch": rmw_bytes / rmw_launches if rmw_launches else None,
             "mean_launch_ms": mean_ms,
             "launches_per_step": rmw_launches / a.steps,
+            # every library pass of the timed region (ZO passes and the DiZO
+            # event's projection passes), per ZO parameter and per step
+            "bytes_per_param_per_step": sum(v["bytes_per_launch"] * v["launches"] for v in summ.values())
+            / (a.steps * r["P"]),
+            "library_launches_per_step": sum(v["launches"] for v in summ.values()) / a.steps,
         },
         "kernels": summ,
         "loss_first_last": [r["losses"][0], r["losses"][-1]] if r["losses"] else None,

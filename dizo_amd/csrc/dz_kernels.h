@@ -83,10 +83,16 @@ constexpr int kCounters = DZ_RMW_COUNTERS;
 constexpr int kCounterStride = 32;  // uint32 slots (128 bytes)
 constexpr int kCounterWords = (kCounters + 1) * kCounterStride;
 
-// Projection kernel geometry: 256 threads x 32 elements (16-bit T: 4 x 16 B,
-// fp32: 8 x 16 B per thread).
-constexpr int kProjThreads = 256;
-constexpr int kProjChunk = 8192;
+// Projection kernel geometry: one workgroup per chunk, each thread 4 (16-bit
+// T) or 8 (fp32) 16-byte vectors of theta and of theta0 per chunk.
+#ifndef DZ_PROJ_THREADS
+#define DZ_PROJ_THREADS 256
+#endif
+#ifndef DZ_PROJ_CHUNK
+#define DZ_PROJ_CHUNK 8192
+#endif
+constexpr int kProjThreads = DZ_PROJ_THREADS;
+constexpr int kProjChunk = DZ_PROJ_CHUNK;
 
 // By-value scalars of one RMW launch.
 struct DzScalars {

@@ -558,6 +558,61 @@ __device__ __forceinline__ void proj_elem(int mode, uint32_t thb, uint32_t t0b, 
   }
 }
 
+// R_T(a - b) and R_T(a * b) for two packed 16-bit lanes of T (both operands
+// in T: the exact difference or product rounded once, which is the
+// reference's fp32 op rounded to T).
+template <int DT>
+__device__ __forceinline__ uint32_t sub_pair(uint32_t a, uint32_t b) {
+  if constexpr (DT == DZ_F16) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(dz_half2, a) - __builtin_bit_cast(dz_half2, b));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(dz_bf2, a) - __builtin_bit_cast(dz_bf2, b));
+  }
+}
+template <int DT>
+__device__ __forceinline__ uint32_t mul_pair(uint32_t a, uint32_t b) {
+  if constexpr (DT == DZ_F16) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(dz_half2, a) * __builtin_bit_cast(dz_half2, b));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(dz_bf2, a) * __builtin_bit_cast(dz_bf2, b));
+  }
+}
+
+// Sum of squares of the two lanes of a packed 16-bit word, low lane first.
+template <int DT>
+__device__ __forceinline__ void acc_sq_pair(uint32_t d, double* acc) {
+  const double d0 = (double)DT_<DT>::to_f(d & 0xffffu);
+  const double d1 = (double)DT_<DT>::to_f(d >> 16);
+  *acc += d0 * d0;
+  *acc += d1 * d1;
+}
+
+// proj_elem for the two 16-bit elements of a word, in packed arithmetic where
+// the reference's op has both operands in T (SUMSQ, APPLY and the subtract /
+// add of REVERSE); alpha2 holds alpha in both lanes. APPLY_F32 is not here
+// (its fp32 alpha keeps v and the sum in fp32).
+template <int DT, int MODE>
+__device__ __forceinline__ uint32_t proj_word16(uint32_t th, uint32_t t0, uint32_t alpha2, float alpha,
+                                                double* acc) {
+  const uint32_t d = sub_pair<DT>(th, t0);
+  if constexpr (MODE == kProjSumsq) {
+    acc_sq_pair<DT>(d, acc);
+    return th;
+  } else {
+    uint32_t v;
+    if constexpr (MODE == kProjApply) {
+      v = mul_pair<DT>(d, alpha2);
+    } else {
+      const float v0 = DT_<DT>::to_f(d & 0xffffu) / alpha;
+      const float v1 = DT_<DT>::to_f(d >> 16) / alpha;
+      v = DT_<DT>::from_f(v0) | (DT_<DT>::from_f(v1) << 16);
+    }
+    const uint32_t nb = add_pair<DT>(v, t0);
+    if constexpr (MODE == kProjReverseSumsq) acc_sq_pair<DT>(sub_pair<DT>(nb, t0), acc);
+    return nb;
+  }
+}
+
 __device__ __forceinline__ double block_sum_f64(double x, double* red) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
@@ -594,32 +649,36 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
   if (ch.n == (uint32_t)kProjChunk && aligned) {
     constexpr int kPer = 16 / kES;  // elements per 16-byte vector
     constexpr int kVecsPerThread = kProjChunk / (kProjThreads * kPer);
-    uint4 vt[kVecsPerThread], va[kVecsPerThread];
+    // alpha in both 16-bit lanes (the ZO modes' alpha is a value of T)
+    const uint32_t alpha2 = (kES == 2 && MODE != kProjApplyF32) ? DT_<DT>::from_f(alpha) * 0x10001u : 0u;
+    dz_u32x4 vt[kVecsPerThread], va[kVecsPerThread];
 #pragma unroll
     for (int u = 0; u < kVecsPerThread; ++u) {
       const size_t off = (size_t)(threadIdx.x + u * kProjThreads) * 16;
-      vt[u] = *(const uint4*)(tp + off);
-      va[u] = *(const uint4*)(ap + off);
+      vt[u] = ld_stream(tp + off);
+      va[u] = ld_stream(ap + off);
     }
 #pragma unroll
     for (int u = 0; u < kVecsPerThread; ++u) {
-      const uint32_t it[4] = {vt[u].x, vt[u].y, vt[u].z, vt[u].w};
-      const uint32_t ia[4] = {va[u].x, va[u].y, va[u].z, va[u].w};
-      uint32_t o[4];
+      dz_u32x4 o;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if constexpr (kES == 2) {
+        if constexpr (kES == 2 && MODE != kProjApplyF32) {
+          o[i] = proj_word16<DT, MODE>(vt[u][i], va[u][i], alpha2, alpha, &acc);
+        } else if constexpr (kES == 2) {
           uint32_t r0, r1;
-          proj_elem<DT>(MODE, it[i] & 0xffffu, ia[i] & 0xffffu, alpha, &r0, &acc);
-          proj_elem<DT>(MODE, it[i] >> 16, ia[i] >> 16, alpha, &r1, &acc);
+          proj_elem<DT>(MODE, vt[u][i] & 0xffffu, va[u][i] & 0xffffu, alpha, &r0, &acc);
+          proj_elem<DT>(MODE, vt[u][i] >> 16, va[u][i] >> 16, alpha, &r1, &acc);
           o[i] = (r0 & 0xffffu) | (r1 << 16);
         } else {
-          proj_elem<DT>(MODE, it[i], ia[i], alpha, &o[i], &acc);
+          uint32_t r;
+          proj_elem<DT>(MODE, vt[u][i], va[u][i], alpha, &r, &acc);
+          o[i] = r;
         }
       }
       if constexpr (MODE != kProjSumsq) {
         const size_t off = (size_t)(threadIdx.x + u * kProjThreads) * 16;
-        *(uint4*)(tp + off) = make_uint4(o[0], o[1], o[2], o[3]);
+        st_stream(tp + off, o);
       }
     }
   } else {
