@@ -39,6 +39,8 @@ What differs from the reference, by design:
 """
 from __future__ import annotations
 
+import json
+import signal
 import warnings
 import weakref
 from collections import OrderedDict
@@ -91,6 +93,10 @@ class ZOArguments:
     # build-specific: ratios tried by ENHANCED=grid (the searched-ratio DiZO
     # event: loss at each ratio, best applied); None = 8 values in [0.5, 1.0]
     dizo_grid: Optional[Tuple[float, ...]] = None
+    # build-specific: append one JSON line per step (step, seed, loss1, loss2,
+    # projected_grad, lr) to this file, written every 50 steps and at the end
+    # (the values stay on the device until then: no extra synchronisation)
+    zo_log_path: Optional[str] = None
 
 
 def layout_z_offsets(numels: Sequence[int]) -> List[int]:
@@ -431,6 +437,7 @@ class ZOTrainerMixin:
         loss1 = self.zo_forward(model, inputs)
         self.zo_perturb_parameters(scaling_factor=-2)
         loss2 = self.zo_forward(model, inputs)
+        self._last_loss2 = loss2
         self.projected_grad = ((loss1 - loss2) / (2 * self.args.zo_eps)).item()
         assert self.args.gradient_accumulation_steps == 1
         if getattr(args, "zo_fuse_restore", True):
@@ -490,6 +497,8 @@ class ZOTrainerMixin:
 
     def zo_close(self) -> None:
         self.zo_flush()
+        if hasattr(self, "flush_log"):
+            self.flush_log()
         if getattr(self, "_graph", None) is not None:
             self._graph.close()
             self._graph = None
@@ -518,6 +527,25 @@ def _anchor_copy(model: torch.nn.Module, exclude_list: Sequence[str]) -> torch.n
     return base
 
 
+class StopOnSignal:
+    """utils.py:291-315 (SIGUSR1Callback): SIGUSR1 (a SLURM stop) or SIGINT sets
+    a flag, and the training loop stops at the end of the current step
+    (ZOTrainer.train). Installs the handlers on construction (main thread);
+    close() puts the previous ones back."""
+
+    def __init__(self, signals=(signal.SIGUSR1, signal.SIGINT)):
+        self.signal_received = False
+        self._prev = {s: signal.signal(s, self.handle_signal) for s in signals}
+
+    def handle_signal(self, signum, frame) -> None:
+        self.signal_received = True
+
+    def close(self) -> None:
+        for s, h in self._prev.items():
+            signal.signal(s, h)
+        self._prev = {}
+
+
 class ZOTrainer(ZOTrainerMixin):
     """Minimal host of the ZO step: the reference's per-step contract
     (trainer.py:1206-1326) without the HF Trainer (no evaluation, saving or
@@ -530,6 +558,8 @@ class ZOTrainer(ZOTrainerMixin):
         self.zo_setup(model, train_dataloader, base_model=base_model)
         self.tr_loss = torch.zeros((), device=self.named_parameters_to_optim[0][1].device)
         self._last_logged = 0
+        self._log_path = getattr(args, "zo_log_path", None)
+        self._log_buf: List[tuple] = []
         self._graph = None
         if getattr(args, "zo_graph", False):
             from .graph import GraphedZOStep
@@ -560,7 +590,9 @@ class ZOTrainer(ZOTrainerMixin):
         model = self.model
         tr_loss_step = self.zo_step(model, inputs)
         self._account(tr_loss_step)
+        lr = self._get_learning_rate()
         self.zo_update(self.args, model)
+        self._log_step(tr_loss_step, self._last_loss2, self.projected_grad, lr)
         self._finish_step(tr_loss_step)
         return tr_loss_step
 
@@ -573,8 +605,10 @@ class ZOTrainer(ZOTrainerMixin):
         lr = self._get_learning_rate()
         tr_loss_step = self._graph.step(inputs, self.zo_random_seed, lr).clone()
         self.projected_grad = None
+        g_dev = self._graph.d_prev_g.clone() if (self.zo_journal is not None or self._log_path) else None
         if self.zo_journal is not None:
-            self.zo_journal.zo(self.zo_random_seed, self._graph.d_prev_g.clone(), lr)
+            self.zo_journal.zo(self.zo_random_seed, g_dev, lr)
+        self._log_step(tr_loss_step, None, g_dev, lr)
         self._account(tr_loss_step)
         if (self.state.global_step + 1) % DIZO_INTERVAL == 0 and args.enhanced:
             self._dizo_event(self.model, self.zo_random_seed)
@@ -582,10 +616,47 @@ class ZOTrainer(ZOTrainerMixin):
         self._finish_step(tr_loss_step)
         return tr_loss_step
 
-    def train(self, batches, max_steps: Optional[int] = None):
+    def _log_step(self, loss1, loss2, g, lr: float) -> None:
+        """Buffers one step's record (device scalars stay on the device)."""
+        if not self._log_path:
+            return
+        self._log_buf.append((self.state.global_step + 1, self.zo_random_seed, loss1, loss2, g, float(lr)))
+        if len(self._log_buf) >= DIZO_INTERVAL:
+            self.flush_log()
+
+    def flush_log(self) -> None:
+        """Appends the buffered step records to zo_log_path as JSON lines."""
+        if not self._log_path or not self._log_buf:
+            return
+
+        def host(x):
+            if x is None:
+                return None
+            return float(x.item()) if torch.is_tensor(x) else float(x)
+
+        with open(self._log_path, "a") as f:
+            for step, seed, l1, l2, g, lr in self._log_buf:
+                f.write(json.dumps({"step": int(step), "seed": int(seed), "loss1": host(l1), "loss2": host(l2),
+                                    "projected_grad": host(g), "lr": lr}) + "\n")
+        self._log_buf = []
+
+    def train(self, batches, max_steps: Optional[int] = None, stop: Optional["StopOnSignal"] = None,
+              checkpoint_dir: Optional[str] = None):
+        """max_steps training steps over `batches`. With `stop`, a received signal
+        ends the run at the end of the current step (trainer.py:1357 with
+        utils.py:307-310); the pending fused work is applied and, given
+        checkpoint_dir, a checkpoint is written (the reference asks for a save
+        there). Returns the step losses."""
         n = max_steps if max_steps is not None else self.args.max_steps
         it = iter(batches)
         for _ in range(n):
             self.training_step(next(it))
+            if stop is not None and stop.signal_received:
+                break
         self.zo_flush()
+        self.flush_log()
+        if stop is not None and stop.signal_received and checkpoint_dir:
+            from .checkpoint import save_checkpoint
+
+            save_checkpoint(self, checkpoint_dir)
         return [float(x) for x in self.loss_list]

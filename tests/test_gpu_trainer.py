@@ -10,6 +10,7 @@ squares, correctly rounded fp32 sqrt, rounded to T); torch.norm itself is
 within one unit in the last place of it (tests/test_gpu_projection.py).
 """
 import copy
+import json
 
 import numpy as np
 import pytest
@@ -360,3 +361,32 @@ def test_graph_steps_with_option_head_match_eager(dt):
     lg, pg = _run_trainer(dt, True, None, 10, batches, option_head=True)
     assert _same(le, lg), f"losses differ: {le} vs {lg}"
     assert all(_same(a, b) for a, b in zip(pe, pg))
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_step_log_records_the_run(graph, tmp_path):
+    """zo_log_path: one JSON line per step with the step's seed, loss1 and
+    projected gradient (the journal's), loss2 on the eager path."""
+    from dizo_amd.synth import Cycle, build_opt, make_batches
+    from dizo_amd.trainer import ZOArguments, ZOTrainer
+    batches = make_batches(3, 4, 512, seed=44, device="cuda", fixed_len=16)
+    model = build_opt("opt-tiny", torch.float16, "cuda", seed=3)
+    path = str(tmp_path / "steps.jsonl")
+    args = ZOArguments(learning_rate=1e-3, zo_eps=1e-3, max_steps=7, zo_graph=graph, zo_journal=True,
+                       zo_log_path=path)
+    np.random.seed(26)
+    tr = ZOTrainer(model, args)
+    losses = tr.train(Cycle(batches), max_steps=7)
+    tr.zo_close()
+    lines = [json.loads(x) for x in open(path)]
+    zo = [op for op in tr.zo_journal.ops if op[0] == "zo"]
+    assert [x["step"] for x in lines] == list(range(1, 8))
+    assert [x["seed"] for x in lines] == [op[1] for op in zo]
+    assert [x["loss1"] for x in lines] == losses
+    assert [x["projected_grad"] for x in lines] == [float(op[2]) if not torch.is_tensor(op[2]) else float(op[2].item())
+                                                   for op in zo]
+    if not graph:
+        for x in lines:
+            g = (torch.tensor(x["loss1"], dtype=torch.float16) - torch.tensor(x["loss2"], dtype=torch.float16))
+            assert x["loss2"] is not None and np.isfinite(x["loss2"])
+            assert abs(float(g) / 2e-3 - x["projected_grad"]) <= abs(x["projected_grad"]) * 1e-3 + 1e-6
