@@ -68,7 +68,8 @@ def load_traffic(kernel: str, workload: str):
         return None
 
 
-def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = False, option_head: bool = False):
+def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = False, option_head: bool = False,
+              enhanced: str = "zo"):
     import numpy as np
     import torch
 
@@ -86,8 +87,8 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = Fa
     torch.cuda.synchronize()
     log(f"[bench] built {shape.name} {dtype} + anchor in {time.perf_counter() - t0:.1f}s; "
         f"mem {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
-    args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=warmup + steps, enhanced="zo", zo_graph=graph,
-                       zo_option_head=option_head)
+    args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=warmup + steps,
+                       enhanced=None if enhanced == "none" else enhanced, zo_graph=graph, zo_option_head=option_head)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches), base_model=base)
     P = sum(p.numel() for _, p in tr.named_parameters_to_optim)
@@ -99,7 +100,8 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = Fa
     torch.cuda.synchronize()
     log(f"[bench] warmup {warmup} steps done")
     tr.kernel_timer = timer
-    tr.dizo_trainer.dizo.kernel_timer = timer
+    if getattr(tr, "dizo_trainer", None) is not None and args.enhanced:
+        tr.dizo_trainer.dizo.kernel_timer = timer
     t_start = time.perf_counter()
     for i in range(steps):
         tr.training_step(next(it))
@@ -110,7 +112,7 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = Fa
     summary = timer.summary()
     tr.zo_close()
     return dict(elapsed=elapsed, P=P, summary=summary, losses=losses, elem_bytes=torch.finfo(dtype).bits // 8,
-                events=sum(1 for k in range(warmup, warmup + steps) if (k + 1) % 50 == 0))
+                events=sum(1 for k in range(warmup, warmup + steps) if (k + 1) % 50 == 0) if args.enhanced else 0)
 
 
 def cpu_baseline(wl_name: str, log=print):
@@ -279,6 +281,9 @@ def main(argv=None):
     ap.add_argument("--kernels", action="store_true", help="per-pass kernel microbench instead of full steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true", help="replay each ZO step as a captured hipGraph")
+    ap.add_argument("--enhanced", default="zo", choices=["zo", "fo", "grid", "none"],
+                    help="DiZO event every 50 steps: ZO gamma search (the reference's dizo.sh), first-order, "
+                         "ratio grid, or none (MeZO)")
     ap.add_argument("--full-logits", action="store_true",
                     help="compute logits at every position, as the reference does (default: only at the option "
                          "positions the loss reads, the same loss)")
@@ -304,7 +309,8 @@ def main(argv=None):
         res = kernel_microbench(a.workload, log=log)
         print(json.dumps({"metric": "ZO pass HBM GB/s", "workload": a.workload, **res}), flush=True)
         return 0
-    r = run_steps(a.workload, a.steps, a.warmup, log=log, graph=a.graph, option_head=not a.full_logits)
+    r = run_steps(a.workload, a.steps, a.warmup, log=log, graph=a.graph, option_head=not a.full_logits,
+                  enhanced=a.enhanced)
     wl = WORKLOADS[a.workload]
     value = a.steps / r["elapsed"]
     summ = r["summary"]
@@ -331,7 +337,7 @@ def main(argv=None):
                                f"candidates, {'seq ' + str(wl['fixed_len']) if wl['fixed_len'] else 'len U[32,64]'}, "
                                f"projection every 50 steps, theta0 resident)",
                    "zo_params": r["P"], "dizo_events_timed": r["events"], "global_batch": 2 * wl["batch"],
-                   "graph": a.graph, "option_head": not a.full_logits,
+                   "graph": a.graph, "option_head": not a.full_logits, "enhanced": a.enhanced,
                    "seq_len": wl["fixed_len"] or wl["max_len"]},
         "roofline": {
             "kernel": "rmw_kernel (perturb -2 / restore+update / restore+update+next perturb)",
