@@ -17,7 +17,9 @@ and learning-rate schedule:
     within 1e-2 (see the test for why not bit for bit);
   * config C2 (kernel passes over the OPT-2.7B trainable set): separate
     passes (+1, -2, +1, update) and fused passes give the same weights bit for
-    bit, and match the reference's expressions on sampled tensors.
+    bit, and match the reference's expressions on sampled tensors;
+  * config C5's scale (OPT-30B bf16): the fused passes and the projection on
+    sampled tensors and groups against the reference's expressions.
 """
 import copy
 
@@ -232,3 +234,66 @@ def test_c2_opt27b_separate_and_fused_passes():
     bad = [named[i][0] for i, (_, p) in enumerate(named) if not _same(p.data, sep[i])]
     assert not bad, f"fused restore+update differs on {len(bad)} tensors, e.g. {bad[:3]}"
     tabs.close()
+
+
+def test_c5_opt30b_bf16_passes_and_projection():
+    """Config C5's scale (OPT-30B bf16: 771 trainable tensors, 29.6 G elements,
+    about 0.9 M tiles per launch; 96 projected groups): after +1, -2 and the
+    fused restore+update+next perturb over the whole set, sampled tensors
+    (first, second, middle, near the end) match the reference's expressions;
+    the projection's norms, apply and reverse+norms on sampled groups match the
+    reference's torch expressions with the library's norm definition."""
+    from dizo_amd import _lib as L
+    from dizo_amd.dizo import DiZO
+    from dizo_amd.synth import build_opt
+    from dizo_amd.table import ProjTable
+    from dizo_amd.trainer import _ZOTables, select_trainable
+    dt, eps, lr = torch.bfloat16, 1e-3, 1e-6
+    g = float(torch.tensor(0.8125, dtype=dt))
+    model = build_opt("opt-30b", dt, "cuda", seed=0)
+    named, exclude = select_trainable(model)
+    assert len(named) == 771 and sum(p.numel() for _, p in named) == 29_614_190_592
+    sample = [0, 1, len(named) // 2, len(named) - 3]
+    before = {i: named[i][1].detach().clone() for i in sample}
+    tabs = _ZOTables(named)
+    (tab, _), = tabs.tables
+    s1, s2 = 2024, 2025
+    tab.perturb(s1, 1.0, eps)
+    tab.perturb(s1, -2.0, eps)
+    tab.restore_update_perturb(s1, s2, eps, g, lr)
+    torch.cuda.synchronize()
+    for i in sample:
+        z1, z2 = tab.export_z(s1, i), tab.export_z(s2, i)
+        ref = [before[i].clone()]
+        R.zo_perturb_parameters_recipe(ref, [z1], 1, eps)
+        R.zo_perturb_parameters_recipe(ref, [z1], -2, eps)
+        R.zo_perturb_parameters_recipe(ref, [z1], 1, eps)
+        R.zo_update_recipe(ref, [z1], g, lr)
+        R.zo_perturb_parameters_recipe(ref, [z2], 1, eps)
+        assert _same(ref[0], named[i][1].data), named[i][0]
+    del before
+    tabs.close()
+    names = DiZO(model, "l2norm", exclude).constraints_name
+    assert len(names) == 96
+    params = dict(model.named_parameters())
+    th = [params[n].data for n in names]
+    t0 = [(t.float() - 1e-3).to(dt) for t in th]
+    ptab = ProjTable(th, t0)
+    norms = torch.empty(96, dtype=dt, device="cuda")
+    ptab.group_sumsq(norm_T=norms)
+    gs = [0, 47, 95]
+    want = torch.stack([_lib_norm(th[i] - t0[i]) for i in gs])
+    assert _same(norms[gs], want)
+    alpha = torch.full((96,), 0.9, dtype=dt, device="cuda")
+    keep = {i: th[i].clone() for i in gs}
+    ptab.project(alpha, L.DZ_PROJ_APPLY)
+    ptab.project(alpha, L.DZ_PROJ_REVERSE_SUMSQ, norm_T=norms)
+    torch.cuda.synchronize()
+    a = alpha[:1]
+    for i in gs:
+        r = (keep[i] - t0[i]) * a + t0[i]
+        r = (r - t0[i]) / a + t0[i]
+        assert _same(th[i], r), names[i]
+    want = torch.stack([_lib_norm(th[i] - t0[i]) for i in gs])
+    assert _same(norms[gs], want)
+    ptab.close()
