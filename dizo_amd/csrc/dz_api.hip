@@ -9,6 +9,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -566,21 +567,24 @@ int32_t dz_group_dot(dz_table* t, const uint64_t* other_ptrs, double* d_dot, flo
   if (rc) return rc;
   if (!t->projection) return fail(DZ_ERR_INVALID, "group_dot needs a projection table");
   if (!other_ptrs) return fail(DZ_ERR_INVALID, "other_ptrs is NULL");
-  if (t->n > dz::kMaxDotGroups)
-    return fail(DZ_ERR_INVALID, "group_dot takes at most " + std::to_string(dz::kMaxDotGroups) + " groups");
-  dz::DzPtrArray other{};
   for (int32_t i = 0; i < t->n; ++i) {
     if (t->numels[i] > 0) {
       rc = check_range(other_ptrs[i], (uint64_t)t->numels[i] * elem_size(t->dtype), "other", i);
       if (rc) return rc;
     }
-    other.p[i] = other_ptrs[i];
   }
   rc = check_group_outputs(t, d_dot, d_dot_f32, nullptr);
   if (rc) return rc;
   hipError_t e = hipSuccess;
-  if (t->nchunks > 0) {
-    e = dz::launch_dot(t->dtype, t->d_chunks, t->nchunks, other, t->d_partials, (hipStream_t)stream);
+  // one launch per batch of kMaxDotGroups groups (a group's chunks are contiguous)
+  for (int32_t g0 = 0; g0 < t->n; g0 += dz::kMaxDotGroups) {
+    const int32_t g1 = std::min<int32_t>(t->n, g0 + dz::kMaxDotGroups);
+    const uint32_t c0 = t->group_begin[g0], c1 = t->group_begin[g1];
+    if (c1 == c0) continue;
+    dz::DzPtrArray other{};
+    for (int32_t i = g0; i < g1; ++i) other.p[i - g0] = other_ptrs[i];
+    e = dz::launch_dot(t->dtype, t->d_chunks + c0, c1 - c0, other, (uint32_t)g0, t->d_partials + c0,
+                       (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "dot kernel launch");
   }
   e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_dot, d_dot_f32, nullptr,

@@ -24,7 +24,8 @@ enum ProjMode : int {
   kProjReverseSumsq = 3,  // REVERSE, then the sums of the new theta
   kProjApplyF32 = 4,      // theta <- R_T(fp32(R(theta - theta0)) * alpha + theta0), alpha fp32
 };
-// Most groups a dot launch takes (their pointers travel as kernel arguments).
+// Most groups one dot launch takes (their pointers travel as kernel
+// arguments); dz_group_dot launches once per batch of groups.
 constexpr int kMaxDotGroups = 128;
 struct DzPtrArray {
   uint64_t p[kMaxDotGroups];
@@ -118,8 +119,10 @@ hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchun
                       hipStream_t st);
 hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, const void* alpha,
                        double* partials, hipStream_t st);
+// Chunks of groups group_base .. group_base + kMaxDotGroups - 1; other.p[i]
+// is the tensor of group group_base + i.
 hipError_t launch_dot(int dtype, const DzChunk* chunks, uint32_t nchunks, const DzPtrArray& other,
-                      double* partials, hipStream_t st);
+                      uint32_t group_base, double* partials, hipStream_t st);
 // take_sqrt: norms (sqrt of the sums) or plain sums in the fp32 / T outputs.
 hipError_t launch_finalize(int dtype, const double* partials, const uint32_t* gbegin, uint32_t ngroups,
                            double* sumsq, float* norm_f32, void* norm_T, bool take_sqrt, hipStream_t st);

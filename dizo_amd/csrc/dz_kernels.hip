@@ -703,7 +703,7 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
 // autograd gives sum(fp32(grad theta') * fp32(delta)) per projected tensor.
 template <int DT>
 __global__ void __launch_bounds__(kProjThreads) dot_kernel(const DzChunk* __restrict__ chunks, DzPtrArray other,
-                                                           double* __restrict__ partials) {
+                                                           uint32_t group_base, double* __restrict__ partials) {
   using S = typename DT_<DT>::S;
   constexpr int kES = (int)sizeof(S);
   __shared__ double red[kProjThreads / 64];
@@ -712,7 +712,7 @@ __global__ void __launch_bounds__(kProjThreads) dot_kernel(const DzChunk* __rest
   const uint32_t grp = ch.meta & kDzMetaGroupMask;
   const S* tp = (const S*)ch.ptr;
   const S* ap = (const S*)ch.aux;
-  const S* op = (const S*)(other.p[grp] + ch.zgroup * (uint64_t)kES);
+  const S* op = (const S*)(other.p[grp - group_base] + ch.zgroup * (uint64_t)kES);
   double acc = 0.0;
   for (uint32_t e = threadIdx.x; e < ch.n; e += kProjThreads) {
     const float d = rt<DT>(DT_<DT>::to_f((uint32_t)tp[e]) - DT_<DT>::to_f((uint32_t)ap[e]));
@@ -857,16 +857,19 @@ hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchu
 }
 
 hipError_t launch_dot(int dtype, const DzChunk* chunks, uint32_t nchunks, const DzPtrArray& other,
-                      double* partials, hipStream_t st) {
+                      uint32_t group_base, double* partials, hipStream_t st) {
   switch (dtype) {
     case DZ_F32:
-      hipLaunchKernelGGL((dot_kernel<DZ_F32>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other, partials);
+      hipLaunchKernelGGL((dot_kernel<DZ_F32>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other,
+                         group_base, partials);
       break;
     case DZ_F16:
-      hipLaunchKernelGGL((dot_kernel<DZ_F16>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other, partials);
+      hipLaunchKernelGGL((dot_kernel<DZ_F16>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other,
+                         group_base, partials);
       break;
     case DZ_BF16:
-      hipLaunchKernelGGL((dot_kernel<DZ_BF16>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other, partials);
+      hipLaunchKernelGGL((dot_kernel<DZ_BF16>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other,
+                         group_base, partials);
       break;
     default:
       return hipErrorInvalidValue;

@@ -160,3 +160,22 @@ def test_group_dot_matches_fp64(dt):
         assert float(dot[g]) == pytest.approx(want, rel=1e-12, abs=1e-300)
         assert float(dotf[g]) == np.float32(float(dot[g]))
     tab.close()
+
+
+def test_group_dot_more_groups_than_one_launch_takes():
+    """200 groups (more than the 128 one dot launch takes): every group's sum
+    against float64 torch, including empty groups at a batch boundary."""
+    from dizo_amd.table import ProjTable
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(6)
+    sizes = [(1000 + 37 * i) if i not in (127, 128) else 0 for i in range(200)]
+    ths = [(torch.randn(n, device=dev, generator=gen) * 0.02).half() for n in sizes]
+    t0s = [(t.float() - 1e-3).half() for t in ths]
+    others = [torch.randn(n, device=dev, generator=gen).half() for n in sizes]
+    dot = torch.empty(200, dtype=torch.float64, device=dev)
+    tab = ProjTable(ths, t0s)
+    tab.group_dot(others, dot)
+    for g in range(200):
+        want = float((others[g].double() * (ths[g] - t0s[g]).double()).sum())
+        assert float(dot[g]) == pytest.approx(want, rel=1e-12, abs=1e-300), g
+    tab.close()
