@@ -150,7 +150,7 @@ int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sum
 
 /* Per group g: d_dot[g] = sum fp32(other_g) * fp32(R_T(theta_g - theta0_g))
  * (fp64 accumulation; d_dot_f32[g] its fp32 rounding), with other_ptrs a host
- * array of n device addresses of tensors shaped like theta_g (n <= 128). The
+ * array of n device addresses of tensors shaped like theta_g. The
  * gradient of the first-order gamma objective with respect to alpha
  * (autograd through trainer.py:428-429 in DiZO.forward, trainer.py:714-741). */
 int32_t dz_group_dot(dz_table* t, const uint64_t* other_ptrs, double* d_dot, float* d_dot_f32,
