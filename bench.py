@@ -269,6 +269,18 @@ def kernel_microbench(wl_name: str, reps: int = 10, log=print):
     for _ in range(2):
         dst.copy_(src)
     torch.cuda.synchronize()
+    # context: the same copy timed (reads and writes copy_bytes: a plain streaming RMW's traffic pattern)
+    ms = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    t = float(np.median(ms))
+    out["device_copy_4GiB"] = {"ms": t, "GBps": 2 * copy_bytes / t / 1e6, "frac": 2 * copy_bytes / t / 1e6 / HBM_PEAK_GBPS}
+    log(f"[kernels] device copy 4 GiB {t:8.3f} ms {2 * copy_bytes / t / 1e6:8.1f} GB/s")
     return {"bytes_per_pass": nbytes, "passes": out, "calibration_copy_bytes": copy_bytes}
 
 
