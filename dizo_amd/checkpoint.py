@@ -368,8 +368,7 @@ def load_checkpoint(trainer, path: str) -> None:
         trainer.tr_loss = torch.tensor(state["tr_loss"], dtype=trainer.tr_loss.dtype, device=trainer.tr_loss.device)
     trainer._last_logged = int(state.get("last_logged", 0))
     if hasattr(trainer, "loss_list"):
-        dev = trainer.named_parameters_to_optim[0][1].device
-        trainer.loss_list = [torch.tensor(x, device=dev) for x in state.get("loss_list", [])]
+        trainer.loss_list = [torch.tensor(x) for x in state.get("loss_list", [])]
     dz_state = state.get("dizo")
     if dz_state is not None:
         dtr = trainer.dizo_trainer
