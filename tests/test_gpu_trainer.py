@@ -390,3 +390,16 @@ def test_step_log_records_the_run(graph, tmp_path):
             g = (torch.tensor(x["loss1"], dtype=torch.float16) - torch.tensor(x["loss2"], dtype=torch.float16))
             assert x["loss2"] is not None and np.isfinite(x["loss2"])
             assert abs(float(g) / 2e-3 - x["projected_grad"]) <= abs(x["projected_grad"]) * 1e-3 + 1e-6
+
+
+@pytest.mark.parametrize("enhanced", ["fo", "grid"])
+def test_graph_steps_with_fo_and_grid_events_match_eager(enhanced):
+    """Captured-graph steps around a first-order or ratio-grid DiZO event (the
+    event runs eagerly between replays) give the eager run's losses and
+    weights bit for bit."""
+    from dizo_amd.synth import make_batches
+    batches = make_batches(5, 4, 512, seed=45, device="cuda", min_len=8, max_len=20)
+    le, pe = _run_trainer(torch.float16, False, enhanced, 53, batches)
+    lg, pg = _run_trainer(torch.float16, True, enhanced, 53, batches)
+    assert _same(le, lg)
+    assert all(_same(a, b) for a, b in zip(pe, pg))

@@ -314,3 +314,28 @@ def test_update_rounds_ties_like_torch_cpu_and_cuda():
     print(f"tie elements {ties}; ROCm torch differs from torch on the CPU on {off} (1M tensor), "
           f"{off_small} (2,560-element tensors)", flush=True)
     tab.close()
+
+
+def test_single_tensor_beyond_2_32_elements():
+    """One fp16 tensor of 2^32 + 8200 elements (8.6 GB), its z offset past 2^32
+    as well: perturb and the fused restore+update+perturb, checked against the
+    oracle on windows at the start, across the 2^32 element boundary and at the
+    ragged end."""
+    from dizo_amd.table import ZOTable
+    n = (1 << 32) + 8200
+    t = torch.zeros(n, dtype=torch.float16, device="cuda")
+    off = 3 << 31  # the tensor's first z index
+    tab = ZOTable([t], z_offsets=[off])
+    seed, eps, g, lr = 99, 1e-3, -1.25, 1e-6
+    tab.perturb(seed, 1.0, eps)
+    tab.restore_update_perturb(seed, seed + 1, eps, g, lr)
+    torch.cuda.synchronize()
+    for start in (0, (1 << 32) - 4096, n - 5000):
+        m = min(9000, n - start)
+        z1 = rng.tensor_z_bits(seed, off + start, m, F16)
+        z2 = rng.tensor_z_bits(seed + 1, off + start, m, F16)
+        th = np.zeros(m, dtype=np.uint16)
+        want = A.perturb(A.restore_update(A.perturb(th, z1, 1, eps, F16), z1, eps, g, lr, F16), z2, 1, eps, F16)
+        got = t[start:start + m].cpu().view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(got, want), start
+    tab.close()
