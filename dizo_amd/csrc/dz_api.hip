@@ -146,12 +146,18 @@ int32_t ensure_device(int dev, DeviceState** out) {
   if (!s.ready) {
     hipError_t e = hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
-    for (int d = 0; d < 3; ++d) {
+    for (int d = 0; d < 3 && e == hipSuccess; ++d) {
       const size_t bytes = (size_t)kDzTabEntries * (size_t)elem_size(d);
       e = hipMalloc(&s.tab[d], bytes);
-      if (e != hipSuccess) return hip_fail(e, "hipMalloc(quantile table)");
-      e = hipMemcpy(s.tab[d], host_table_ptr(d), bytes, hipMemcpyHostToDevice);
-      if (e != hipSuccess) return hip_fail(e, "hipMemcpy(quantile table)");
+      if (e == hipSuccess) e = hipMemcpy(s.tab[d], host_table_ptr(d), bytes, hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) {
+      // leave the state as it was, so that a later call starts over
+      for (void*& p : s.tab) {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+      }
+      return hip_fail(e, "quantile table upload");
     }
     s.ready = true;
   }
@@ -289,6 +295,49 @@ void build_chunks(const dz_table* t, uint32_t elems, std::vector<DzChunk>* out,
   }
 }
 
+// Rejects a table in which a range the kernels write (theta) overlaps another
+// registered range: within one launch the tiles of both would be read and
+// written by different workgroups in no fixed order. Anchors are only read
+// and may overlap each other (one anchor shared by several groups).
+int32_t check_no_overlap(const dz_table* t) {
+  struct Range {
+    uint64_t lo, hi;
+    bool write;
+    int32_t idx;
+  };
+  const int es = elem_size(t->dtype);
+  std::vector<Range> r;
+  r.reserve((size_t)t->n * (t->projection ? 2 : 1));
+  for (int32_t i = 0; i < t->n; ++i) {
+    if (t->numels[i] == 0) continue;
+    const uint64_t bytes = (uint64_t)t->numels[i] * es;
+    r.push_back({t->ptrs[i], t->ptrs[i] + bytes, true, i});
+    if (t->projection) r.push_back({t->aux[i], t->aux[i] + bytes, false, i});
+  }
+  std::sort(r.begin(), r.end(), [](const Range& a, const Range& b) { return a.lo < b.lo; });
+  // Sorted by start, a range overlaps an earlier one iff it starts below the
+  // largest end seen so far (of any range, or of a written one).
+  uint64_t end_any = 0, end_write = 0;
+  int32_t who_any = -1, who_write = -1;
+  for (const Range& x : r) {
+    const bool clash = x.write ? (x.lo < end_any) : (x.lo < end_write);
+    if (clash) {
+      const int32_t other = x.write ? who_any : who_write;
+      return fail(DZ_ERR_INVALID, "the memory of tensor " + std::to_string(x.idx) + " overlaps that of tensor " +
+                                      std::to_string(other) + (t->projection ? " (or its anchor)" : ""));
+    }
+    if (x.hi > end_any) {
+      end_any = x.hi;
+      who_any = x.idx;
+    }
+    if (x.write && x.hi > end_write) {
+      end_write = x.hi;
+      who_write = x.idx;
+    }
+  }
+  return DZ_OK;
+}
+
 hipError_t upload_chunks(const std::vector<DzChunk>& v, DzChunk** d) {
   if (v.empty()) return hipSuccess;
   hipError_t e = hipMalloc(d, v.size() * sizeof(DzChunk));
@@ -388,6 +437,11 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
   if (total_tiles >= 0xffffffffull) {
     free_table(t);
     return fail(DZ_ERR_INVALID, "too many tiles");
+  }
+  rc = check_no_overlap(t);
+  if (rc) {
+    free_table(t);
+    return rc;
   }
   std::vector<DzChunk> chunks;
   build_chunks(t, t->chunk_elems, &chunks, &t->group_begin);

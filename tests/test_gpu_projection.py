@@ -121,6 +121,16 @@ def test_empty_and_rejects():
     with pytest.raises(DzError):
         ProjTable(a, [torch.zeros(0, device=dev), torch.zeros(11, device=dev)])
     tab.close()
+    # a written tensor may not overlap another tensor or any anchor; anchors may be shared
+    base = torch.zeros(40, device=dev)
+    anchor = torch.zeros(10, device=dev)
+    with pytest.raises(DzError, match="overlaps"):
+        ProjTable([base[:10], base[5:15]], [anchor, anchor])
+    with pytest.raises(DzError, match="overlaps"):
+        ProjTable([base[:10], base[10:20]], [anchor, base[15:25]])
+    with pytest.raises(DzError, match="overlaps"):
+        ProjTable([base[:10]], [base[:10]])
+    ProjTable([base[:10], base[10:20]], [anchor, anchor]).close()
 
 
 @pytest.mark.parametrize("dt", DTS)

@@ -275,6 +275,15 @@ def test_rejects_bad_inputs():
         ZOTable([torch.zeros(4, device="cuda"), torch.zeros(4, device="cuda", dtype=torch.float16)])
     with pytest.raises(DzError):
         ZOTable([torch.zeros(4, 4, device="cuda").t()])  # non-contiguous
+    # overlapping tensors would be read and written by two workgroups at once
+    base = torch.zeros(100, device="cuda")
+    with pytest.raises(DzError, match="overlaps"):
+        ZOTable([base[:60], base[50:]])
+    with pytest.raises(DzError, match="overlaps"):
+        ZOTable([base, base[10:20]])
+    with pytest.raises(DzError, match="overlaps"):
+        ZOTable([base, base])
+    ZOTable([base[:50], base[50:]]).close()  # adjacent is fine
 
 
 def test_update_rounds_ties_like_torch_cpu_and_cuda():
