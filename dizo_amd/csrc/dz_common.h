@@ -77,9 +77,17 @@ DZ_HD DzU4 dz_philox4x32(DzU4 c, uint32_t k0, uint32_t k1) {
     dz_mulhilo32(0xCD9E8D57u, c.z, &lo1, &hi1);
     DzU4 n;
 #if defined(__HIP_DEVICE_COMPILE__)
-    // gfx950 three-input bitwise op; truth table 0x96 is a ^ b ^ c
-    n.x = __builtin_amdgcn_bitop3_b32(hi1, c.y, k0, 0x96);
-    n.z = __builtin_amdgcn_bitop3_b32(hi0, c.w, k1, 0x96);
+    if (r == 0) {
+      // Plain xors: with a uniform counter word 1 and stream, n.x is uniform
+      // and stays on the scalar unit (the bitop3 builtin is vector-only), and
+      // so does round 1's product of it.
+      n.x = hi1 ^ c.y ^ k0;
+      n.z = hi0 ^ c.w ^ k1;
+    } else {
+      // gfx950 three-input bitwise op; truth table 0x96 is a ^ b ^ c
+      n.x = __builtin_amdgcn_bitop3_b32(hi1, c.y, k0, 0x96);
+      n.z = __builtin_amdgcn_bitop3_b32(hi0, c.w, k1, 0x96);
+    }
 #else
     n.x = hi1 ^ c.y ^ k0;
     n.z = hi0 ^ c.w ^ k1;
@@ -93,13 +101,19 @@ DZ_HD DzU4 dz_philox4x32(DzU4 c, uint32_t k0, uint32_t k1) {
   return c;
 }
 
-DZ_HD DzU4 dz_philox_group(uint64_t seed, uint32_t stream, uint64_t q) {
+// The block of counter q = q_hi * 2^32 + q_lo, with the two words passed
+// apart (a caller whose q_hi is uniform across a wave keeps it scalar).
+DZ_HD DzU4 dz_philox_counter(uint64_t seed, uint32_t stream, uint32_t q_lo, uint32_t q_hi) {
   DzU4 c;
-  c.x = (uint32_t)q;
-  c.y = (uint32_t)(q >> 32);
+  c.x = q_lo;
+  c.y = q_hi;
   c.z = stream;
   c.w = 0u;
   return dz_philox4x32<10>(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+}
+
+DZ_HD DzU4 dz_philox_group(uint64_t seed, uint32_t stream, uint64_t q) {
+  return dz_philox_counter(seed, stream, (uint32_t)q, (uint32_t)(q >> 32));
 }
 
 // 16-bit field j (0..7) of a Philox output block.

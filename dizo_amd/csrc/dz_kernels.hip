@@ -337,11 +337,25 @@ __device__ __forceinline__ void compute_store_tile(const DzChunk& ch, const Tile
   // All Philox blocks of the tile first: G (or 2G) independent 10-round
   // chains the scheduler can interleave.
   DzU4 w[G], w2[G];
+  // The counters of the tile's groups are zgroup + [0, G * kRmwThreads). When
+  // their high words agree (the low word does not wrap inside the tile), the
+  // high word is wave-uniform: round 0's xor and round 1's first product then
+  // run on the scalar unit, one v_mad_u64_u32 less per block.
+  const uint32_t q_lo = (uint32_t)ch.zgroup, q_hi = (uint32_t)(ch.zgroup >> 32);
+  if (q_lo <= 0xffffffffu - (uint32_t)(G * kRmwThreads - 1)) {
 #pragma unroll
-  for (int u = 0; u < G; ++u) {
-    const uint64_t q = ch.zgroup + threadIdx.x + u * kRmwThreads;
-    w[u] = dz_philox_group(sc.seed, kDzStreamParam, q);
-    w2[u] = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, q) : w[u];
+    for (int u = 0; u < G; ++u) {
+      const uint32_t lo = q_lo + threadIdx.x + u * kRmwThreads;
+      w[u] = dz_philox_counter(sc.seed, kDzStreamParam, lo, q_hi);
+      w2[u] = kTwoSeeds ? dz_philox_counter(sc.seed2, kDzStreamParam, lo, q_hi) : w[u];
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const uint64_t q = ch.zgroup + threadIdx.x + u * kRmwThreads;
+      w[u] = dz_philox_group(sc.seed, kDzStreamParam, q);
+      w2[u] = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, q) : w[u];
+    }
   }
   if constexpr (DT != DZ_F32) {
 #pragma unroll

@@ -348,3 +348,45 @@ def test_single_tensor_beyond_2_32_elements():
         got = t[start:start + m].cpu().view(torch.int16).numpy().view(np.uint16)
         assert np.array_equal(got, want), start
     tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_tiles_across_the_2_32_counter_boundary(dt):
+    """Philox counters q = e >> 3 past 2^32: z offsets put one tile of each tile
+    size across q = 2^32 (its counters' high word changes inside the tile),
+    the tiles before it at high word 0 and the tiles after it at high word 1.
+    Every mode (perturb, update, restore+update, restore+update+next perturb),
+    every element against the oracle."""
+    from dizo_amd.table import ZOTable
+    sizes = [200_000, 70_001]
+    # the first tensor starts 5000 groups below q = 2^32; the second 904 groups
+    # below q = 2^33, so its first tile crosses at once
+    offs = [(1 << 35) - 8 * 5000, (1 << 36) - 8 * 904]
+    host = [random_theta(n, dt, 40 + i) for i, n in enumerate(sizes)]
+    dev = torch.device("cuda", 0)
+    tensors = [to_torch(b, dt, dev) for b in host]
+    tab = ZOTable(tensors, z_offsets=offs)
+    seed, seed2, eps, g, lr = 512, 513, 1e-3, 0.75, 1e-3
+    z1 = [rng.tensor_z_bits(seed, o, n, dt) for o, n in zip(offs, sizes)]
+    z2 = [rng.tensor_z_bits(seed2, o, n, dt) for o, n in zip(offs, sizes)]
+    want = list(host)
+
+    def check(what):
+        torch.cuda.synchronize()
+        for i, t in enumerate(tensors):
+            assert_bits_equal(to_bits(t).ravel(), want[i], dt, f"{what}, tensor {i}")
+
+    tab.perturb(seed, 1.0, eps)
+    want = [A.perturb(w, z, 1, eps, dt) for w, z in zip(want, z1)]
+    check("perturb")
+    tab.update(seed, g, lr)
+    want = [A.update(w, z, g, lr, dt) for w, z in zip(want, z1)]
+    check("update")
+    tab.restore_update(seed, eps, g, lr)
+    want = [A.restore_update(w, z, eps, g, lr, dt) for w, z in zip(want, z1)]
+    check("restore+update")
+    tab.restore_update_perturb(seed, seed2, eps, g, lr)
+    want = [A.perturb(A.restore_update(w, z, eps, g, lr, dt), zz, 1, eps, dt)
+            for w, z, zz in zip(want, z1, z2)]
+    check("restore+update+next perturb")
+    tab.close()
