@@ -646,11 +646,26 @@ class ZOTrainer(ZOTrainerMixin):
         ends the run at the end of the current step (trainer.py:1357 with
         utils.py:307-310); the pending fused work is applied and, given
         checkpoint_dir, a checkpoint is written (the reference asks for a save
-        there). Returns the step losses."""
+        there). A re-iterable `batches` (a list, a DataLoader) is run again
+        from its start when it ends, one epoch after another, as the
+        reference's loop does (trainer.py:1186-1206); a one-shot iterator ends
+        the run when it is exhausted. Returns the step losses."""
         n = max_steps if max_steps is not None else self.args.max_steps
         it = iter(batches)
+        one_shot = it is batches
         for _ in range(n):
-            self.training_step(next(it))
+            try:
+                inputs = next(it)
+            except StopIteration:
+                if one_shot:
+                    break
+                it = iter(batches)
+                self.state.epoch += 1.0
+                try:
+                    inputs = next(it)
+                except StopIteration:
+                    raise DzError("train: batches is empty") from None
+            self.training_step(inputs)
             if stop is not None and stop.signal_received:
                 break
         self.zo_flush()

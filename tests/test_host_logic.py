@@ -102,3 +102,29 @@ def test_step_log_writes_json_lines(cpu_trainer):
     assert [x["step"] for x in lines] == [1, 2, 3]
     assert [x["seed"] for x in lines] == [100, 101, 102]
     assert lines[2] == {"step": 3, "seed": 102, "loss1": 2.5, "loss2": 0.25, "projected_grad": 3.0, "lr": 1e-6}
+
+
+def test_train_runs_epochs_over_a_short_batch_list(cpu_trainer):
+    """A list shorter than max_steps is run again from its start (one epoch
+    after another, as the reference's loop does); a one-shot iterator ends the
+    run when it is exhausted; an empty list is an error."""
+    from dizo_amd._lib import DzError
+    tr = cpu_trainer
+    seen = []
+
+    def fake_step(inputs):
+        seen.append(inputs)
+        tr.state.global_step += 1
+        tr.loss_list.append(torch.tensor(0.5))
+        return torch.tensor(0.5)
+
+    tr.training_step = fake_step
+    tr.zo_flush = lambda: None
+    tr.train(["a", "b", "c"], max_steps=7)
+    assert seen == ["a", "b", "c", "a", "b", "c", "a"]
+    assert tr.state.epoch == 2.0
+    seen.clear()
+    tr.train(iter(["x", "y"]), max_steps=5)
+    assert seen == ["x", "y"]
+    with pytest.raises(DzError):
+        tr.train([], max_steps=2)
