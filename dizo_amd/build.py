@@ -54,5 +54,29 @@ def build(verbose: bool = False, out: str = LIB_PATH, extra_flags=()) -> str:
     return out
 
 
+C_HOST_SRC = os.path.join(CSRC, "zo_step_host.c")
+C_HOST_PATH = os.path.join(os.path.dirname(LIB_PATH), "zo_step_host")
+
+
+def build_c_host(verbose: bool = False, lib: str = LIB_PATH, out: str = C_HOST_PATH) -> str:
+    """Compiles csrc/zo_step_host.c, a C99 host of the ZO step through the C ABI
+    (gcc, HIP runtime C API, linked with the library), and returns its path."""
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    include = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+    libdir = os.path.dirname(os.path.abspath(lib))
+    cmd = ["gcc", "-std=c99", "-O2", "-Wall", "-Werror", "-D__HIP_PLATFORM_AMD__",
+           "-I", include, "-I", os.path.join(rocm, "include"), C_HOST_SRC, "-o", out + ".tmp",
+           "-L", libdir, "-ldizo_amd", "-Wl,-rpath,$ORIGIN", "-L", os.path.join(rocm, "lib"), "-lamdhip64",
+           f"-Wl,-rpath,{os.path.join(rocm, 'lib')}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"gcc failed ({res.returncode}):\n{res.stderr}")
+    os.replace(out + ".tmp", out)
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(build_c_host(verbose=True))
