@@ -390,3 +390,52 @@ def test_tiles_across_the_2_32_counter_boundary(dt):
             for w, z, zz in zip(want, z1, z2)]
     check("restore+update+next perturb")
     tab.close()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_special_values_follow_ieee_like_the_oracle(dt):
+    """theta holding +-inf, NaN, +-0, the largest finite value and the smallest
+    subnormal, among ordinary values: every RMW mode, then the projection's
+    apply and reverse with a supplied alpha, against the oracle (NaN equal to
+    NaN, as torch's expressions give NaN there too)."""
+    from dizo_amd._lib import DZ_PROJ_APPLY, DZ_PROJ_REVERSE
+    from dizo_amd.table import ProjTable, ZOTable
+    big = {F16: 65504.0, BF16: 3.3895314e38, F32: 3.4028235e38}[dt]
+    tiny = {F16: 5.96e-8, BF16: 9.2e-41, F32: 1.4e-45}[dt]
+    specials = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, big, -big, tiny, -tiny], dtype=np.float32)
+    n = 40_003
+    x = (np.random.default_rng(5).standard_normal(n) * 0.02).astype(np.float32)
+    x[::97] = np.resize(specials, x[::97].size)
+    h0 = A.from_f32(x, dt)
+    dev = torch.device("cuda", 0)
+    t = to_torch(h0, dt, dev)
+    tab = ZOTable([t])
+    seed, seed2, eps, g, lr = 77, 78, 1e-3, 2.5, 1e-3
+    z = rng.tensor_z_bits(seed, 0, n, dt)
+    z2 = rng.tensor_z_bits(seed2, 0, n, dt)
+    want = A.perturb(h0, z, 1, eps, dt)
+    tab.perturb(seed, 1.0, eps)
+    assert_bits_equal(to_bits(t).ravel(), want, dt, "perturb")
+    want = A.update(want, z, g, lr, dt)
+    tab.update(seed, g, lr)
+    assert_bits_equal(to_bits(t).ravel(), want, dt, "update")
+    want = A.restore_update(want, z, eps, g, lr, dt)
+    tab.restore_update(seed, eps, g, lr)
+    assert_bits_equal(to_bits(t).ravel(), want, dt, "restore+update")
+    want = A.perturb(A.restore_update(want, z, eps, g, lr, dt), z2, 1, eps, dt)
+    tab.restore_update_perturb(seed, seed2, eps, g, lr)
+    assert_bits_equal(to_bits(t).ravel(), want, dt, "restore+update+next perturb")
+    tab.close()
+    # projection: theta0 is the starting theta (finite where theta is, so
+    # inf - theta0 = inf and NaN stays NaN)
+    anchor = to_torch(h0, dt, dev)
+    ptab = ProjTable([t], [anchor])
+    alpha_bits = A.from_f32(np.float32(0.75), dt).reshape(1)
+    alpha = to_torch(alpha_bits, dt, dev)
+    ptab.project(alpha, DZ_PROJ_APPLY)
+    want = A.apply(want, h0, alpha_bits, dt)
+    assert_bits_equal(to_bits(t).ravel(), want, dt, "apply")
+    ptab.project(alpha, DZ_PROJ_REVERSE)
+    want = A.reverse(want, h0, alpha_bits, dt)
+    assert_bits_equal(to_bits(t).ravel(), want, dt, "reverse")
+    ptab.close()
