@@ -206,7 +206,7 @@ struct dz_table {
   DzChunk* d_chunks = nullptr;
   uint32_t* d_group_begin = nullptr;
   double* d_partials = nullptr;
-  uint32_t* d_counters = nullptr;  // RMW work counters (ZO tables)
+  uint32_t* d_counters = nullptr;  // work counters of the persistent RMW / projection kernels
   DeviceState* dev = nullptr;
 };
 
@@ -251,6 +251,13 @@ uint32_t rmw_grid(const dz_table* t, int mode, uint32_t ntiles) {
   const uint32_t per_cu = dz::rmw_lds_table_bytes(t->dtype, mode) <= 65536 ? (uint32_t)DZ_RMW_NARROW_WG_PER_CU : 1u;
   const uint32_t g = per_cu * (uint32_t)t->dev->cus;
   return ntiles < g ? ntiles : g;
+}
+
+// Persistent grid of a projection launch: DZ_PROJ_WG_PER_CU workgroups per
+// CU, but no more than there are chunks.
+uint32_t proj_grid(const dz_table* t) {
+  const uint32_t g = (uint32_t)DZ_PROJ_WG_PER_CU * (uint32_t)t->dev->cus;
+  return t->nchunks < g ? t->nchunks : g;
 }
 
 int32_t rmw(dz_table* t, int mode, const dz::DzScalars& s, const dz::DzScalarPtrs& p, void* stream) {
@@ -465,8 +472,8 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
                     hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMalloc(&t->d_partials, (size_t)(t->nchunks ? t->nchunks : 1) * sizeof(double));
   }
-  if (e == hipSuccess && !t->projection) {
-    // zeroed once here; every RMW launch leaves them at zero again
+  if (e == hipSuccess) {
+    // zeroed once here; every RMW and projection launch leaves them at zero again
     e = hipMalloc(&t->d_counters, dz::kCounterWords * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(t->d_counters, 0, dz::kCounterWords * sizeof(uint32_t));
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -581,8 +588,8 @@ int32_t dz_group_sumsq(dz_table* t, double* d_sumsq, float* d_norm_f32, void* d_
   if (rc) return rc;
   hipError_t e = hipSuccess;
   if (t->nchunks > 0) {
-    e = dz::launch_proj(t->dtype, dz::kProjSumsq, t->d_chunks, t->nchunks, nullptr, t->d_partials,
-                        (hipStream_t)stream);
+    e = dz::launch_proj(t->dtype, dz::kProjSumsq, t->d_chunks, t->nchunks, (uint32_t)t->n, proj_grid(t),
+                        nullptr, t->d_partials, t->d_counters, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "sumsq kernel launch");
   }
   e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_sumsq, d_norm_f32,
@@ -604,8 +611,8 @@ int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sum
   if (!rc) rc = check_group_outputs(t, d_sumsq, d_norm_f32, d_norm_T);
   if (rc) return rc;
   if (t->nchunks > 0) {
-    hipError_t e = dz::launch_proj(t->dtype, mode, t->d_chunks, t->nchunks, d_alpha, t->d_partials,
-                                   (hipStream_t)stream);
+    hipError_t e = dz::launch_proj(t->dtype, mode, t->d_chunks, t->nchunks, (uint32_t)t->n, proj_grid(t),
+                                   d_alpha, t->d_partials, t->d_counters, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "projection kernel launch");
   }
   if (mode == DZ_PROJ_REVERSE_SUMSQ) {

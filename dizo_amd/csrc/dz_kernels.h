@@ -84,16 +84,23 @@ constexpr int kCounters = DZ_RMW_COUNTERS;
 constexpr int kCounterStride = 32;  // uint32 slots (128 bytes)
 constexpr int kCounterWords = (kCounters + 1) * kCounterStride;
 
-// Projection kernel geometry: one workgroup per chunk, each thread 4 (16-bit
-// T) or 8 (fp32) 16-byte vectors of theta and of theta0 per chunk.
+// Projection kernel geometry: persistent 1024-thread workgroups, DZ_PROJ_WG_PER_CU
+// per CU, taking 32768-element chunks (64 KB of theta and 64 KB of theta0 in
+// 16-bit T): each thread 4 (16-bit T) or 8 (fp32) 16-byte vectors of each.
 #ifndef DZ_PROJ_THREADS
-#define DZ_PROJ_THREADS 256
+#define DZ_PROJ_THREADS 1024
 #endif
 #ifndef DZ_PROJ_CHUNK
-#define DZ_PROJ_CHUNK 8192
+#define DZ_PROJ_CHUNK 32768
+#endif
+#ifndef DZ_PROJ_WG_PER_CU
+#define DZ_PROJ_WG_PER_CU 1
 #endif
 constexpr int kProjThreads = DZ_PROJ_THREADS;
 constexpr int kProjChunk = DZ_PROJ_CHUNK;
+// Groups whose alphas a projection workgroup keeps in LDS (16 KB of fp32);
+// beyond that each chunk reads its group's alpha from memory.
+constexpr int kProjAlphaLds = 4096;
 
 // By-value scalars of one RMW launch.
 struct DzScalars {
@@ -117,8 +124,10 @@ struct DzScalarPtrs {
 hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
                       const void* qtab, const DzScalars& s, const DzScalarPtrs& p, uint32_t* counters,
                       hipStream_t st);
-hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, const void* alpha,
-                       double* partials, hipStream_t st);
+// Persistent: `grid` workgroups share the chunks through `counters` (zero
+// before the launch; the launch leaves them at zero).
+hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t ngroups,
+                       uint32_t grid, const void* alpha, double* partials, uint32_t* counters, hipStream_t st);
 // Chunks of groups group_base .. group_base + kMaxDotGroups - 1; other.p[i]
 // is the tensor of group group_base + i.
 hipError_t launch_dot(int dtype, const DzChunk* chunks, uint32_t nchunks, const DzPtrArray& other,

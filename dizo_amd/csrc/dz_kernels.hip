@@ -265,12 +265,17 @@ __device__ __forceinline__ uint32_t apply_one(uint32_t th, uint32_t h, uint32_t 
 typedef uint32_t dz_u32x4 __attribute__((ext_vector_type(4)));
 
 // Streaming 16-byte accesses: theta is touched once per pass, so loads and
-// stores carry the non-temporal hint.
+// stores carry the non-temporal hint. The pointers are global-memory ones
+// (address space 1): the accesses then compile to global_load / global_store,
+// which count only against the vector-memory wait counter. As generic (FLAT)
+// accesses they would also count against the LDS counter, and every wait for
+// an LDS table lookup would then wait for the tile loads in flight as well.
+typedef __attribute__((address_space(1))) dz_u32x4 dz_global_u32x4;
 __device__ __forceinline__ dz_u32x4 ld_stream(const void* p) {
-  return __builtin_nontemporal_load((const dz_u32x4*)p);
+  return __builtin_nontemporal_load((const dz_global_u32x4*)(uintptr_t)p);
 }
 __device__ __forceinline__ void st_stream(void* p, dz_u32x4 v) {
-  __builtin_nontemporal_store(v, (dz_u32x4*)p);
+  __builtin_nontemporal_store(v, (dz_global_u32x4*)(uintptr_t)p);
 }
 
 // Wave-uniform copy of a 32-bit value in a scalar register.
@@ -290,6 +295,18 @@ __device__ __forceinline__ DzChunk uniform_chunk(const DzChunk& c) {
   u.ptr = rfl_u64(c.ptr);
   u.aux = 0;
   u.zgroup = rfl_u64(c.zgroup);
+  u.n = rfl_u32(c.n);
+  u.meta = rfl_u32(c.meta);
+  return u;
+}
+
+// The same for a projection chunk, whose anchor address (aux) is used and
+// whose z group is not.
+__device__ __forceinline__ DzChunk uniform_proj_chunk(const DzChunk& c) {
+  DzChunk u;
+  u.ptr = rfl_u64(c.ptr);
+  u.aux = rfl_u64(c.aux);
+  u.zgroup = 0;
   u.n = rfl_u32(c.n);
   u.meta = rfl_u32(c.meta);
   return u;
@@ -541,8 +558,9 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
 //   APPLY_F32      theta <- R_T(fp32(R_T(theta - theta0)) * alpha + theta0) with an fp32 alpha:
 //                  the first-order path's apply (trainer.py:428-436 with gamma an fp32
 //                  Parameter, so v and temp stay fp32 and copy_ rounds once)
-// One chunk per workgroup; squares and sums in fp64 (exact squares of the
-// fp32-widened differences); fixed reduction order, so results are deterministic.
+// Each chunk is processed by one workgroup; squares and sums in fp64 (exact
+// squares of the fp32-widened differences) in a fixed reduction order, so the
+// per-chunk partials, and the group sums built from them, are deterministic.
 // ---------------------------------------------------------------------------
 template <int DT>
 __device__ __forceinline__ void proj_elem(int mode, uint32_t thb, uint32_t t0b, float alpha,
@@ -640,22 +658,13 @@ __device__ __forceinline__ double block_sum_f64(double x, double* red) {
   return t;
 }
 
+// One chunk of a projection launch: the chunk's elements read (theta and
+// theta0), updated and written back, and for the SUMSQ modes the chunk's
+// partial sum (fixed reduction order) stored at *partial.
 template <int DT, int MODE>
-__global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __restrict__ chunks,
-                                                            const void* __restrict__ alpha_T,
-                                                            double* __restrict__ partials) {
+__device__ __forceinline__ void proj_chunk(const DzChunk& ch, float alpha, double* partial, double* red) {
   using S = typename DT_<DT>::S;
   constexpr int kES = (int)sizeof(S);
-  __shared__ double red[kProjThreads / 64];
-  const uint32_t c = blockIdx.x;
-  const DzChunk ch = chunks[c];
-  const uint32_t grp = ch.meta & kDzMetaGroupMask;
-  float alpha = 0.0f;
-  if constexpr (MODE == kProjApplyF32) {
-    alpha = ((const float*)alpha_T)[grp];
-  } else if constexpr (MODE != kProjSumsq) {
-    alpha = DT_<DT>::to_f((uint32_t)((const S*)alpha_T)[grp]);
-  }
   char* tp = (char*)ch.ptr;
   const char* ap = (const char*)ch.aux;
   double acc = 0.0;
@@ -706,7 +715,96 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
   }
   if constexpr (MODE == kProjSumsq || MODE == kProjReverseSumsq) {
     const double t = block_sum_f64(acc, red);
-    if (threadIdx.x == 0) partials[c] = t;
+    if (threadIdx.x == 0) *partial = t;
+  }
+}
+
+// alpha of a group: one value of T, or fp32 for APPLY_F32; none for SUMSQ.
+template <int DT, int MODE>
+__device__ __forceinline__ float group_alpha(const void* __restrict__ alpha_T, uint32_t grp) {
+  if constexpr (MODE == kProjSumsq) {
+    return 0.0f;
+  } else if constexpr (MODE == kProjApplyF32) {
+    return ((const float*)alpha_T)[grp];
+  } else {
+    return DT_<DT>::to_f((uint32_t)((const typename DT_<DT>::S*)alpha_T)[grp]);
+  }
+}
+
+// Persistent projection kernel: one 1024-thread workgroup per CU takes chunks
+// from the table's work counters, as the RMW kernel does (counter j of the K
+// in use hands out chunks j, j + K, ...). The groups' alphas are copied to
+// LDS once (up to kProjAlphaLds groups; beyond that each chunk reads its
+// group's alpha from memory). Wave 0 keeps a pipeline: while chunk k streams,
+// lane 0 takes the index of chunk k + 3 and the wave loads the descriptor of
+// chunk k + 2 with scalar loads, so no descriptor latency sits between two
+// chunks. The last workgroup to finish resets the counters.
+template <int DT, int MODE>
+__global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __restrict__ chunks, uint32_t nchunks,
+                                                            uint32_t ngroups, const void* __restrict__ alpha_T,
+                                                            double* __restrict__ partials,
+                                                            uint32_t* __restrict__ counters) {
+  __shared__ double red[kProjThreads / 64];
+  __shared__ uint32_t sidx[4];   // chunk indices of k .. k + 3 (ring)
+  __shared__ DzChunk sdesc[3];   // descriptors of k .. k + 2
+  __shared__ float salpha[MODE == kProjSumsq ? 1 : kProjAlphaLds];
+  const bool alpha_in_lds = MODE != kProjSumsq && ngroups <= (uint32_t)kProjAlphaLds;
+  if (alpha_in_lds) {
+    for (uint32_t g = threadIdx.x; g < ngroups; g += kProjThreads) salpha[g] = group_alpha<DT, MODE>(alpha_T, g);
+  }
+  const uint32_t ncnt = rfl_u32(max(1u, min((uint32_t)kCounters, gridDim.x >> 3)));
+  const uint32_t j = rfl_u32((blockIdx.x >> 3) % ncnt);
+  uint32_t* mine = counters + j * kCounterStride;
+  const uint64_t nch = nchunks;
+  if (threadIdx.x == 0) {
+    for (int i = 0; i < 3; ++i) sidx[i] = (uint32_t)min((uint64_t)atomicAdd(mine, 1u) * ncnt + j, nch);
+    for (int i = 0; i < 2; ++i)
+      if (sidx[i] < nchunks) sdesc[i] = chunks[sidx[i]];
+  }
+  __syncthreads();
+  for (uint32_t k = 0;; ++k) {
+    const uint32_t c = sidx[k % 4];
+    if (c >= nchunks) break;
+    const DzChunk ch = uniform_proj_chunk(sdesc[k % 3]);
+    const uint32_t grp = ch.meta & kDzMetaGroupMask;
+    const float alpha = MODE == kProjSumsq ? 0.0f
+                        : alpha_in_lds     ? salpha[grp]
+                                           : group_alpha<DT, MODE>(alpha_T, grp);
+    uint32_t grabbed = 0;
+    uint64_t n_ptr = 0, n_aux = 0;
+    uint32_t n_n = 0, n_meta = 0;
+    bool have_desc = false;
+    if ((rfl_u32(threadIdx.x) >> 6) == 0) {  // wave 0 (uniform branch)
+      const uint32_t cd = rfl_u32(sidx[(k + 2) % 4]);
+      if (threadIdx.x == 0) grabbed = atomicAdd(mine, 1u);
+      if (cd < nchunks) {
+        const DzChunk* src = chunks + cd;
+        n_ptr = src->ptr;
+        n_aux = src->aux;
+        n_n = src->n;
+        n_meta = src->meta;
+        have_desc = true;
+      }
+    }
+    proj_chunk<DT, MODE>(ch, alpha, partials + c, red);
+    if (threadIdx.x == 0) {
+      sidx[(k + 3) % 4] = (uint32_t)min((uint64_t)grabbed * ncnt + j, nch);
+      if (have_desc) {
+        DzChunk& d = sdesc[(k + 2) % 3];
+        d.ptr = n_ptr;
+        d.aux = n_aux;
+        d.zgroup = 0;
+        d.n = n_n;
+        d.meta = n_meta;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const uint32_t done = atomicAdd(counters + kCounters * kCounterStride, 1u);
+    if (done == gridDim.x - 1) {
+      for (int i = 0; i <= kCounters; ++i) atomicExch(counters + i * kCounterStride, 0u);
+    }
   }
 }
 
@@ -831,28 +929,29 @@ hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchun
 }
 
 template <int DT>
-static hipError_t launch_proj_dt(int mode, const DzChunk* chunks, uint32_t nchunks, const void* alpha,
-                                 double* partials, hipStream_t st) {
+static hipError_t launch_proj_dt(int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t ngroups,
+                                 uint32_t grid, const void* alpha, double* partials, uint32_t* counters,
+                                 hipStream_t st) {
   switch (mode) {
     case kProjSumsq:
-      hipLaunchKernelGGL((proj_kernel<DT, kProjSumsq>), dim3(nchunks), dim3(kProjThreads), 0, st,
-                         chunks, alpha, partials);
+      hipLaunchKernelGGL((proj_kernel<DT, kProjSumsq>), dim3(grid), dim3(kProjThreads), 0, st, chunks, nchunks,
+                         ngroups, alpha, partials, counters);
       break;
     case kProjApply:
-      hipLaunchKernelGGL((proj_kernel<DT, kProjApply>), dim3(nchunks), dim3(kProjThreads), 0, st,
-                         chunks, alpha, partials);
+      hipLaunchKernelGGL((proj_kernel<DT, kProjApply>), dim3(grid), dim3(kProjThreads), 0, st, chunks, nchunks,
+                         ngroups, alpha, partials, counters);
       break;
     case kProjReverse:
-      hipLaunchKernelGGL((proj_kernel<DT, kProjReverse>), dim3(nchunks), dim3(kProjThreads), 0,
-                         st, chunks, alpha, partials);
+      hipLaunchKernelGGL((proj_kernel<DT, kProjReverse>), dim3(grid), dim3(kProjThreads), 0, st, chunks, nchunks,
+                         ngroups, alpha, partials, counters);
       break;
     case kProjReverseSumsq:
-      hipLaunchKernelGGL((proj_kernel<DT, kProjReverseSumsq>), dim3(nchunks), dim3(kProjThreads),
-                         0, st, chunks, alpha, partials);
+      hipLaunchKernelGGL((proj_kernel<DT, kProjReverseSumsq>), dim3(grid), dim3(kProjThreads), 0, st, chunks,
+                         nchunks, ngroups, alpha, partials, counters);
       break;
     case kProjApplyF32:
-      hipLaunchKernelGGL((proj_kernel<DT, kProjApplyF32>), dim3(nchunks), dim3(kProjThreads), 0,
-                         st, chunks, alpha, partials);
+      hipLaunchKernelGGL((proj_kernel<DT, kProjApplyF32>), dim3(grid), dim3(kProjThreads), 0, st, chunks, nchunks,
+                         ngroups, alpha, partials, counters);
       break;
     default:
       return hipErrorInvalidValue;
@@ -860,12 +959,15 @@ static hipError_t launch_proj_dt(int mode, const DzChunk* chunks, uint32_t nchun
   return hipGetLastError();
 }
 
-hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, const void* alpha,
-                       double* partials, hipStream_t st) {
+hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t ngroups,
+                       uint32_t grid, const void* alpha, double* partials, uint32_t* counters, hipStream_t st) {
   switch (dtype) {
-    case DZ_F32: return launch_proj_dt<DZ_F32>(mode, chunks, nchunks, alpha, partials, st);
-    case DZ_F16: return launch_proj_dt<DZ_F16>(mode, chunks, nchunks, alpha, partials, st);
-    case DZ_BF16: return launch_proj_dt<DZ_BF16>(mode, chunks, nchunks, alpha, partials, st);
+    case DZ_F32:
+      return launch_proj_dt<DZ_F32>(mode, chunks, nchunks, ngroups, grid, alpha, partials, counters, st);
+    case DZ_F16:
+      return launch_proj_dt<DZ_F16>(mode, chunks, nchunks, ngroups, grid, alpha, partials, counters, st);
+    case DZ_BF16:
+      return launch_proj_dt<DZ_BF16>(mode, chunks, nchunks, ngroups, grid, alpha, partials, counters, st);
     default: return hipErrorInvalidValue;
   }
 }

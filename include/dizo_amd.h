@@ -130,6 +130,8 @@ int32_t dz_philox(uint64_t seed, uint32_t stream_id, uint64_t q0, int64_t n, uin
                   void* stream);
 
 /* ---- DiZO projection (trainer.py:405-465, 564-614) ----------------------- */
+/* As for the ZO launches, launches on one projection table share its work
+ * counters: order them on one stream. */
 
 /* Per group g: d_sumsq[g] = sum fp32(R(theta-theta0))^2 (fp64 accumulation),
  * d_norm_f32[g] = sqrt_f32(fp32(sumsq)), d_norm_T[g] = R_T(norm): the
