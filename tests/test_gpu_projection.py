@@ -12,7 +12,8 @@ from tests._util import DT_TORCH, assert_bits_equal, random_theta, to_bits, to_t
 pytestmark = pytest.mark.gpu
 
 DTS = [F16, BF16, F32]
-SIZES = [8192, 8191, 8193, 5, 64 * 64 * 5 + 3, 300000]
+# around the projection chunk (32768 elements) and its multiples, tiny, ragged and many-chunk groups
+SIZES = [32768, 32767, 32769, 5, 64 * 64 * 5 + 3, 300000, 65536 + 8, 8191]
 
 
 def _groups(dt, seed, sizes=SIZES, rel=1e-2):
@@ -89,7 +90,7 @@ def test_apply_reverse_match_torch_on_device(dt):
     """apply_constraints / reverse_constraints of the reference run by ROCm torch."""
     from dizo_amd._lib import DZ_PROJ_APPLY, DZ_PROJ_REVERSE
     from dizo_amd.table import ProjTable
-    ths, t0s, th_h, t0_h = _groups(dt, 9, sizes=[8192, 4099, 70000])
+    ths, t0s, th_h, t0_h = _groups(dt, 9, sizes=[32768, 4099, 70000])
     ref = [t.clone() for t in ths]
     G = len(ths)
     gammas = [0.9 * torch.norm(ths[g] - t0s[g]) for g in range(G)]
@@ -139,7 +140,7 @@ def test_apply_f32_alpha_matches_torch(dt):
     (theta - theta0) * alpha + theta0 with alpha float32 of shape (1,), copied into T."""
     from dizo_amd._lib import DZ_PROJ_APPLY_F32ALPHA
     from dizo_amd.table import ProjTable
-    ths, t0s, _, _ = _groups(dt, 13, sizes=[8192, 4099, 70000, 7])
+    ths, t0s, _, _ = _groups(dt, 13, sizes=[32768, 4099, 70000, 7, 32769])
     ref = [t.clone() for t in ths]
     G = len(ths)
     alphas = torch.tensor(np.linspace(0.5, 1.3, G), dtype=torch.float32, device=ths[0].device)
@@ -156,7 +157,7 @@ def test_group_dot_matches_fp64(dt):
     """group_dot: sum fp32(other) * fp32(R(theta - theta0)) per group, fp64 accumulation,
     against the same sum formed in float64 by torch (up to summation order)."""
     from dizo_amd.table import ProjTable
-    ths, t0s, _, _ = _groups(dt, 21, sizes=[8192, 8191, 300000, 5, 0])
+    ths, t0s, _, _ = _groups(dt, 21, sizes=[32768, 32767, 300000, 5, 0, 8191])
     gen = torch.Generator(device="cuda").manual_seed(5)
     others = [torch.randn(t.numel(), device=t.device, generator=gen).to(DT_TORCH[dt]) for t in ths]
     G = len(ths)
@@ -188,4 +189,36 @@ def test_group_dot_more_groups_than_one_launch_takes():
     for g in range(200):
         want = float((others[g].double() * (ths[g] - t0s[g]).double()).sum())
         assert float(dot[g]) == pytest.approx(want, rel=1e-12, abs=1e-300), g
+    tab.close()
+
+
+@pytest.mark.parametrize("dt", [F16, F32])
+def test_more_groups_than_the_lds_alpha_table(dt):
+    """More groups (4100) than a projection workgroup keeps alphas for in LDS
+    (4096): each chunk then reads its group's alpha from memory. Apply, reverse
+    and the group norms against the oracle, on views of one buffer."""
+    from dizo_amd._lib import DZ_PROJ_APPLY, DZ_PROJ_REVERSE_SUMSQ
+    from dizo_amd.table import ProjTable
+    G, n = 4100, 37
+    dev = torch.device("cuda", 0)
+    r = np.random.default_rng(3)
+    t0_all = random_theta(G * n, dt, 7, with_edges=False)
+    th_all = from_f32(to_f32(t0_all, dt) + (r.standard_normal(G * n) * 2e-4).astype(np.float32), dt)
+    th_buf, t0_buf = to_torch(th_all, dt, dev), to_torch(t0_all, dt, dev)
+    ths = [th_buf[g * n:(g + 1) * n] for g in range(G)]
+    t0s = [t0_buf[g * n:(g + 1) * n] for g in range(G)]
+    alphas = from_f32(np.linspace(0.6, 1.2, G).astype(np.float32), dt)
+    tab = ProjTable(ths, t0s)
+    tab.project(to_torch(alphas, dt, dev), DZ_PROJ_APPLY)
+    got = to_bits(th_buf)
+    want = np.concatenate([A.apply(th_all[g * n:(g + 1) * n], t0_all[g * n:(g + 1) * n], alphas[g:g + 1], dt)
+                           for g in range(G)])
+    assert_bits_equal(got, want, dt, "apply")
+    sumsq = torch.empty(G, dtype=torch.float64, device=dev)
+    tab.project(to_torch(alphas, dt, dev), DZ_PROJ_REVERSE_SUMSQ, sumsq=sumsq)
+    rev = [A.reverse(want[g * n:(g + 1) * n], t0_all[g * n:(g + 1) * n], alphas[g:g + 1], dt) for g in range(G)]
+    assert_bits_equal(to_bits(th_buf), np.concatenate(rev), dt, "reverse")
+    s = sumsq.cpu().numpy()
+    for g in range(0, G, 97):
+        assert s[g] == pytest.approx(A.group_sumsq(rev[g], t0_all[g * n:(g + 1) * n], dt), rel=1e-12), g
     tab.close()
