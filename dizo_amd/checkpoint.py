@@ -296,7 +296,11 @@ def save_checkpoint(trainer, path: str) -> None:
         anchors = dict(trainer.base_model.named_parameters())
         for n in dtr.dizo.constraints_name:
             tensors["anchor:" + n] = anchors[n].detach().contiguous().cpu()
-    save_file(tensors, os.path.join(path, "theta.safetensors"))
+    # each file is written to a temporary name and renamed into place, so an
+    # interrupted save never leaves a partial file beside an older state
+    tmp = os.path.join(path, "theta.safetensors.tmp")
+    save_file(tensors, tmp)
+    os.replace(tmp, os.path.join(path, "theta.safetensors"))
     sched = trainer.lr_scheduler
     state: Dict[str, Any] = {
         "format": STATE_FORMAT, "version": VERSION,
