@@ -285,7 +285,10 @@ def _load_adam_state(opt: torch.optim.Optimizer, d: Dict[str, Any], device) -> N
 
 def save_checkpoint(trainer, path: str) -> None:
     """Writes theta, the run state and the journal of a ZOTrainerMixin host
-    (call between steps; pending fused work is applied first)."""
+    (call between steps; pending fused work is applied first). Each file is
+    replaced atomically, but the files are replaced one after another: save
+    into a fresh directory (one per step, say) so that an interrupted save
+    cannot leave files of two saves side by side."""
     from safetensors.torch import save_file
 
     trainer.zo_flush()
