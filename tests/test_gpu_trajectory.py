@@ -22,6 +22,7 @@ and learning-rate schedule:
     sampled tensors and groups against the reference's expressions.
 """
 import copy
+import sys
 
 import numpy as np
 import pytest
@@ -46,6 +47,21 @@ def _lib_norm(t: torch.Tensor) -> torch.Tensor:
     return torch.sqrt(s.double()).float().to(t.dtype)
 
 
+def _reporter(capsys):
+    """A progress callback that prints every 50 steps with pytest's output
+    capture suspended, so a long run shows that it is moving."""
+    def report(what: str, k: int, steps: int) -> None:
+        if (k + 1) % 50 == 0 or k + 1 == steps:
+            with capsys.disabled():
+                sys.stdout.write(f"  [{what}] step {k + 1}/{steps}\n")
+                sys.stdout.flush()
+    return report
+
+
+def _quiet(what: str, k: int, steps: int) -> None:
+    pass
+
+
 def _ref_forward(model, batch):
     from dizo_amd.trainer import forward_wrap_with_option_len
     model.eval()
@@ -53,7 +69,7 @@ def _ref_forward(model, batch):
         return forward_wrap_with_option_len(model, **batch, return_dict=True).loss.detach()
 
 
-def _library_run(shape, dt, batches, steps, lr0, eps, seed=5):
+def _library_run(shape, dt, batches, steps, lr0, eps, seed=5, progress=_quiet):
     """The library trainer (ENHANCED=zo, fused passes). Returns the trainer (kept
     open for export_z), its losses, its model and a copy of the initial model."""
     from dizo_amd.synth import Cycle, build_opt
@@ -63,13 +79,16 @@ def _library_run(shape, dt, batches, steps, lr0, eps, seed=5):
     args = ZOArguments(learning_rate=lr0, zo_eps=eps, max_steps=steps, enhanced="zo")
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches))
-    losses = [tr.training_step(batches[k % len(batches)]).reshape(()).clone() for k in range(steps)]
+    losses = []
+    for k in range(steps):
+        losses.append(tr.training_step(batches[k % len(batches)]).reshape(()).clone())
+        progress(f"library {shape}", k, steps)
     tr.zo_flush()
     torch.cuda.synchronize()
     return tr, losses, model, init
 
 
-def _reference_run(tr, init, dt, batches, steps, lr0, eps, norm, recipe=False):
+def _reference_run(tr, init, dt, batches, steps, lr0, eps, norm, recipe=False, progress=_quiet):
     """The reference's expressions on a copy of the initial model, fed the z and
     gamma noise the library exports. recipe: the perturbation and update
     evaluated in the recipe form (exact products rounded as torch's CPU and
@@ -104,6 +123,7 @@ def _reference_run(tr, init, dt, batches, steps, lr0, eps, norm, recipe=False):
         update(params_b, zs, g, A.zo_lr(lr0, k, steps))
         del zs
         losses.append(l1)
+        progress("reference" + (" recipe" if recipe else ""), k, steps)
         if (k + 1) % 50 == 0:
             pb = dict(model_b.named_parameters())
             p0 = dict(anchor_b.named_parameters())
@@ -140,7 +160,7 @@ def test_200_steps_with_four_dizo_events_bit_exact(dt):
     tr.zo_close()
 
 
-def test_c3_shape_200_step_loss_trajectory():
+def test_c3_shape_200_step_loss_trajectory(capsys):
     """Config C3's shape (OPT-2.7B fp16, batch 16 x 2, lengths U[32, 64], lr 1e-6,
     DiZO events at global steps 49/99/149/199).
 
@@ -163,11 +183,13 @@ def test_c3_shape_200_step_loss_trajectory():
     updates. That run is reported and bounded at 1e-2."""
     from dizo_amd.synth import make_batches
     batches = make_batches(8, 16, 50272, seed=82, device="cuda", min_len=32, max_len=64)
-    tr, la, ma, init = _library_run("opt-2.7b", torch.float16, batches, 200, 1e-6, 1e-3)
-    lb, mb, gb = _reference_run(tr, init, torch.float16, batches, 200, 1e-6, 1e-3, _lib_norm, recipe=True)
+    report = _reporter(capsys)
+    tr, la, ma, init = _library_run("opt-2.7b", torch.float16, batches, 200, 1e-6, 1e-3, progress=report)
+    lb, mb, gb = _reference_run(tr, init, torch.float16, batches, 200, 1e-6, 1e-3, _lib_norm, recipe=True,
+                                progress=report)
     _assert_bit_exact(tr, la, ma, lb, mb, gb)
     del mb
-    lt, mt, gt = _reference_run(tr, init, torch.float16, batches, 200, 1e-6, 1e-3, torch.norm)
+    lt, mt, gt = _reference_run(tr, init, torch.float16, batches, 200, 1e-6, 1e-3, torch.norm, progress=report)
     a = torch.stack(la).double().cpu()
     t = torch.stack(lt).double().cpu()
     worst = float((a - t).abs().max())
@@ -178,7 +200,8 @@ def test_c3_shape_200_step_loss_trajectory():
     assert worst <= 1e-2, f"max loss difference {worst} over 200 steps"
     del mt
     # the recipe form with torch.norm: what torch.norm's fp32 accumulation alone changes
-    lc, mc, gc = _reference_run(tr, init, torch.float16, batches, 200, 1e-6, 1e-3, torch.norm, recipe=True)
+    lc, mc, gc = _reference_run(tr, init, torch.float16, batches, 200, 1e-6, 1e-3, torch.norm, recipe=True,
+                                progress=report)
     c = torch.stack(lc).double().cpu()
     worst_c = float((a - c).abs().max())
     same_c = int((_bits(torch.stack(la)) == _bits(torch.stack(lc))).sum())
