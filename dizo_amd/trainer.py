@@ -179,7 +179,8 @@ def shift_option_labels(input_ids: torch.Tensor, option_len, pad_id: int,
     L = input_ids.shape[1]
     first = 1 if window is None else L - window + 1  # first target position
     labels = torch.clone(input_ids)[..., first:].contiguous()
-    labels.masked_fill_(labels == pad_id, -100)
+    if pad_id is not None:  # a config without a pad id (LLaMA) masks nothing, as `labels == None` does
+        labels.masked_fill_(labels == pad_id, -100)
     if option_len is not None:
         ol = torch.as_tensor(option_len, device=labels.device).reshape(-1, 1)
         pos = torch.arange(first - 1, L - 1, device=labels.device).reshape(1, -1)

@@ -403,3 +403,50 @@ def test_graph_steps_with_fo_and_grid_events_match_eager(enhanced):
     lg, pg = _run_trainer(torch.float16, True, enhanced, 53, batches)
     assert _same(le, lg)
     assert all(_same(a, b) for a, b in zip(pe, pg))
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_llama_zo_steps_match_reference(dt):
+    """Another model family through the drop-in (the reference loads any causal
+    LM, run.py:157-181): a tiny random-init LLaMA with no pad id. Its first
+    parameter is not OPT's decoder embedding, so, as trainer.py:1153-1155
+    decides, every trainable tensor (embedding included) is optimised. Five
+    MeZO steps against the reference's expressions, bit for bit."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from dizo_amd.synth import make_batches
+    from dizo_amd.trainer import ZOArguments, ZOTrainer, select_trainable
+
+    torch.manual_seed(4)
+    cfg = LlamaConfig(vocab_size=512, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=64,
+                      pad_token_id=None)
+    model_a = LlamaForCausalLM(cfg).to(dtype=dt, device="cuda").eval()
+    model_b = copy.deepcopy(model_a)
+    batches = make_batches(5, 4, 512, seed=6, device="cuda", min_len=8, max_len=20)
+    steps, lr0, eps = 5, 1e-3, 1e-3
+    np.random.seed(26)
+    tr = ZOTrainer(model_a, ZOArguments(learning_rate=lr0, zo_eps=eps, max_steps=steps, enhanced=None))
+    assert tr.named_parameters_to_optim[0][0] == "model.embed_tokens.weight"
+    losses_a = [tr.training_step(batches[k]) for k in range(steps)]
+    tr.zo_flush()
+
+    np.random.seed(26)
+    named_b, _ = select_trainable(model_b)
+    names = [n for n, _ in named_b]
+    params_b = [p for _, p in named_b]
+    for k in range(steps):
+        seed = np.random.randint(1000000000)
+        zs = [tr.export_z(n, seed) for n in names]
+        R.zo_perturb_parameters(params_b, zs, 1, eps)
+        l1 = _ref_forward(model_b, batches[k])
+        R.zo_perturb_parameters(params_b, zs, -2, eps)
+        l2 = _ref_forward(model_b, batches[k])
+        g = R.projected_grad(l1, l2, eps)
+        R.zo_perturb_parameters(params_b, zs, 1, eps)
+        R.zo_update(params_b, zs, g, A.zo_lr(lr0, k, steps))
+        assert _same(losses_a[k], l1), f"step {k}: loss {losses_a[k]} vs {l1}"
+    pa = dict(model_a.named_parameters())
+    bad = [n for n, p in zip(names, params_b) if not _same(pa[n].data, p.data)]
+    assert not bad, f"{len(bad)} parameters differ after {steps} steps, e.g. {bad[:3]}"
+    tr.zo_close()

@@ -204,3 +204,35 @@ def test_loss_without_kv_cache_is_identical(tiny_model):
         lc = tiny_model(input_ids=b["input_ids"], attention_mask=b["attention_mask"], use_cache=True).logits
     assert torch.equal(a, c)
     assert torch.equal(la, lc)
+
+
+def test_llama_without_pad_id_matches_bruteforce():
+    """Another model family through the same forward (the reference loads any
+    causal LM, run.py:157-181): a tiny random-init LLaMA whose config has no
+    pad id. The reference's `labels == None` masks nothing; so does the
+    library. Full logits and the option-position window, against the
+    brute-force oracle."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from dizo_amd.synth import make_batch
+    from dizo_amd.trainer import forward_wrap_with_option_len
+
+    torch.manual_seed(3)
+    cfg = LlamaConfig(vocab_size=512, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=64,
+                      pad_token_id=None)
+    m = LlamaForCausalLM(cfg).eval()
+    assert m.config.pad_token_id is None
+    gen = torch.Generator().manual_seed(11)
+    b = make_batch(3, 512, gen=gen, min_len=5, max_len=12)
+    b["attention_mask"] = torch.ones_like(b["input_ids"])  # no padding in this family's batches
+    with torch.no_grad():
+        full = forward_wrap_with_option_len(m, **b, return_dict=True).loss
+        logits = m(input_ids=b["input_ids"], attention_mask=b["attention_mask"]).logits
+        m.dz_option_head = True
+        head = forward_wrap_with_option_len(m, **b, return_dict=True).loss
+        m.dz_option_head = False
+    want = OL.classification_loss(logits.double().numpy(), b["input_ids"].numpy(), b["labels"].tolist(),
+                                  b["option_len"].tolist(), b["num_options"].tolist(), None)
+    assert float(full) == pytest.approx(want, rel=1e-5, abs=1e-6)
+    assert float(head) == pytest.approx(want, rel=1e-5, abs=1e-6)
