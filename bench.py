@@ -9,7 +9,11 @@ of 128 random tokens, theta0 anchor resident in HBM), synthetic random-init
 weights and synthetic token batches already resident in HBM. The loss's
 forward computes logits only at the option positions the classification loss
 reads (HF's logits_to_keep; the same loss); --full-logits computes them at
-every position as the reference does.
+every position as the reference does. Each decoder layer's fc1 + ReLU runs as
+one GEMM with a ReLU epilogue and its k/v/q projections as one GEMM (values
+bit-identical to HF's layer at the C3 and C4 shapes; at C5's the fused k/v/q
+GEMM runs another hipBLASLt kernel and can differ in the last bit);
+--hf-layers runs HF's layer code as it is.
 
 Prints one JSON line. `roofline` is the dominant library kernel (the
 multi-tensor perturb / restore+update read-modify-write): algorithmic bytes
@@ -18,7 +22,7 @@ around every launch in the timed region. `cpu_baseline` times the
 reference's expressions (the oracle's torch restatement) on the host cores
 over a bounded sample and scales it to steps/s.
 
-  python bench.py [--gpus 1] [--steps 50] [--warmup 3] [--workload c4] [--graph] [--full-logits]
+  python bench.py [--gpus 1] [--steps 50] [--warmup 3] [--workload c4] [--graph] [--full-logits] [--hf-layers]
   python bench.py --kernels [--workload c4]     # per-pass kernel microbench (config C2 style)
 """
 from __future__ import annotations
@@ -69,7 +73,7 @@ def load_traffic(kernel: str, workload: str):
 
 
 def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = False, option_head: bool = False,
-              enhanced: str = "zo"):
+              enhanced: str = "zo", fused: bool = False):
     import numpy as np
     import torch
 
@@ -88,7 +92,8 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = Fa
     log(f"[bench] built {shape.name} {dtype} + anchor in {time.perf_counter() - t0:.1f}s; "
         f"mem {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
     args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=warmup + steps,
-                       enhanced=None if enhanced == "none" else enhanced, zo_graph=graph, zo_option_head=option_head)
+                       enhanced=None if enhanced == "none" else enhanced, zo_graph=graph, zo_option_head=option_head,
+                       zo_fused_mlp=fused, zo_fused_qkv=fused)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches), base_model=base)
     P = sum(p.numel() for _, p in tr.named_parameters_to_optim)
@@ -299,6 +304,9 @@ def main(argv=None):
     ap.add_argument("--full-logits", action="store_true",
                     help="compute logits at every position, as the reference does (default: only at the option "
                          "positions the loss reads, the same loss)")
+    ap.add_argument("--hf-layers", action="store_true",
+                    help="run HF's decoder layer code as it is (default: fc1 + ReLU as one GEMM with a ReLU "
+                         "epilogue, k/v/q as one GEMM; the same values at the bench shapes)")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the DiZO step path is measured on a "
@@ -322,7 +330,7 @@ def main(argv=None):
         print(json.dumps({"metric": "ZO pass HBM GB/s", "workload": a.workload, **res}), flush=True)
         return 0
     r = run_steps(a.workload, a.steps, a.warmup, log=log, graph=a.graph, option_head=not a.full_logits,
-                  enhanced=a.enhanced)
+                  enhanced=a.enhanced, fused=not a.hf_layers)
     wl = WORKLOADS[a.workload]
     value = a.steps / r["elapsed"]
     summ = r["summary"]
@@ -349,7 +357,8 @@ def main(argv=None):
                                f"candidates, {'seq ' + str(wl['fixed_len']) if wl['fixed_len'] else 'len U[32,64]'}, "
                                f"projection every 50 steps, theta0 resident)",
                    "zo_params": r["P"], "dizo_events_timed": r["events"], "global_batch": 2 * wl["batch"],
-                   "graph": a.graph, "option_head": not a.full_logits, "enhanced": a.enhanced,
+                   "graph": a.graph, "option_head": not a.full_logits, "fused_gemms": not a.hf_layers,
+                   "enhanced": a.enhanced,
                    "seq_len": wl["fixed_len"] or wl["max_len"]},
         "roofline": {
             "kernel": "rmw_kernel (perturb -2 / restore+update / restore+update+next perturb)",

@@ -86,6 +86,12 @@ class ZOArguments:
     # classification loss reads (HF's logits_to_keep) instead of at every
     # position; the loss agrees with the full-logit one to rounding
     zo_option_head: bool = False
+    # build-specific: run each OPT decoder layer's fc1 + ReLU as one GEMM with
+    # a ReLU epilogue, and its k/v/q projections as one GEMM over a [k; v; q]
+    # weight buffer, when no autograd graph is recorded (dizo_amd.fused_layers);
+    # the same values where hipBLASLt runs one kernel family for both shapes
+    zo_fused_mlp: bool = False
+    zo_fused_qkv: bool = False
     # build-specific: keep a journal of every pass that changes the trainable
     # tensors (seed, g, lr per step; DiZO projections), for exact replay and
     # checkpoints (dizo_amd.checkpoint)
@@ -324,9 +330,17 @@ class ZOTrainerMixin:
         self.lr_scheduler = torch.optim.lr_scheduler.LambdaLR(
             optimizer, lambda step: 1 - self.state.global_step / (2 * args.max_steps))
         self.named_parameters_to_optim, self.exclude_list = select_trainable(model)
-        if args.enhanced in ("zo", "fo", "grid"):
-            if base_model is None:
-                base_model = _anchor_copy(model, self.exclude_list)
+        enhanced = args.enhanced in ("zo", "fo", "grid")
+        if enhanced and base_model is None:
+            base_model = _anchor_copy(model, self.exclude_list)
+        # the fused q/k/v layout moves those weights into new buffers: after the
+        # anchor copy, before any table records parameter addresses
+        if getattr(args, "zo_fused_mlp", False) or getattr(args, "zo_fused_qkv", False):
+            from .fused_layers import fuse_forward
+
+            fuse_forward(model, mlp=bool(getattr(args, "zo_fused_mlp", False)),
+                         qkv=bool(getattr(args, "zo_fused_qkv", False)))
+        if enhanced:
             self.base_model = base_model
             self.dizo_trainer = dizo_trainer(base_model, train_dataloader, "l2norm", 0.1, 10, self.exclude_list)
             self.dizo_trainer.bind_model(model)
