@@ -13,7 +13,10 @@ every position as the reference does. Each decoder layer's fc1 + ReLU runs as
 one GEMM with a ReLU epilogue and its k/v/q projections as one GEMM (values
 bit-identical to HF's layer at the C3 and C4 shapes; at C5's the fused k/v/q
 GEMM runs another hipBLASLt kernel and can differ in the last bit);
---hf-layers runs HF's layer code as it is.
+--hf-layers runs HF's layer code as it is. With the fused layers, an
+unpadded batch's causal attention runs through the library's MFMA kernel
+(dz_attention_causal, q scaling included; not bit-identical to SDPA, within
+its rounding); --sdpa keeps SDPA.
 
 Prints one JSON line. `roofline` is the dominant library kernel (the
 multi-tensor perturb / restore+update read-modify-write): algorithmic bytes
@@ -22,7 +25,7 @@ around every launch in the timed region. `cpu_baseline` times the
 reference's expressions (the oracle's torch restatement) on the host cores
 over a bounded sample and scales it to steps/s.
 
-  python bench.py [--gpus 1] [--steps 50] [--warmup 3] [--workload c4] [--graph] [--full-logits] [--hf-layers]
+  python bench.py [--gpus 1] [--steps 50] [--warmup 3] [--workload c4] [--graph] [--full-logits] [--hf-layers] [--sdpa]
   python bench.py --kernels [--workload c4]     # per-pass kernel microbench (config C2 style)
 """
 from __future__ import annotations
@@ -73,7 +76,7 @@ def load_traffic(kernel: str, workload: str):
 
 
 def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = False, option_head: bool = False,
-              enhanced: str = "zo", fused: bool = False):
+              enhanced: str = "zo", fused: bool = False, attention: bool = False):
     import numpy as np
     import torch
 
@@ -93,7 +96,7 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = Fa
         f"mem {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
     args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=warmup + steps,
                        enhanced=None if enhanced == "none" else enhanced, zo_graph=graph, zo_option_head=option_head,
-                       zo_fused_mlp=fused, zo_fused_qkv=fused)
+                       zo_fused_mlp=fused, zo_fused_qkv=fused, zo_fused_attention=fused and attention)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches), base_model=base)
     P = sum(p.numel() for _, p in tr.named_parameters_to_optim)
@@ -307,6 +310,9 @@ def main(argv=None):
     ap.add_argument("--hf-layers", action="store_true",
                     help="run HF's decoder layer code as it is (default: fc1 + ReLU as one GEMM with a ReLU "
                          "epilogue, k/v/q as one GEMM; the same values at the bench shapes)")
+    ap.add_argument("--sdpa", action="store_true",
+                    help="keep SDPA's attention (default with the fused layers: the library's causal attention "
+                         "kernel for unpadded batches)")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the DiZO step path is measured on a "
@@ -330,7 +336,7 @@ def main(argv=None):
         print(json.dumps({"metric": "ZO pass HBM GB/s", "workload": a.workload, **res}), flush=True)
         return 0
     r = run_steps(a.workload, a.steps, a.warmup, log=log, graph=a.graph, option_head=not a.full_logits,
-                  enhanced=a.enhanced, fused=not a.hf_layers)
+                  enhanced=a.enhanced, fused=not a.hf_layers, attention=not a.sdpa)
     wl = WORKLOADS[a.workload]
     value = a.steps / r["elapsed"]
     summ = r["summary"]
@@ -358,6 +364,7 @@ def main(argv=None):
                                f"projection every 50 steps, theta0 resident)",
                    "zo_params": r["P"], "dizo_events_timed": r["events"], "global_batch": 2 * wl["batch"],
                    "graph": a.graph, "option_head": not a.full_logits, "fused_gemms": not a.hf_layers,
+                   "attention": "sdpa" if (a.hf_layers or a.sdpa) else "dz_attention_causal (unpadded batches)",
                    "enhanced": a.enhanced,
                    "seq_len": wl["fixed_len"] or wl["max_len"]},
         "roofline": {

@@ -59,6 +59,8 @@ SIGNATURES = {
     "dz_group_sumsq": (_i32, [_p, _p, _p, _p, _p]),
     "dz_project": (_i32, [_p, _p, _i32, _p, _p, _p, _p]),
     "dz_group_dot": (_i32, [_p, _p, _p, _p, _p]),
+    "dz_attention_causal": (_i32, [_i32, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32,
+                                   _i32, _f32, _p]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,246 @@
+// Causal self-attention of an unpadded batch (the ZO step's forwards, which
+// run without autograd), for 16-bit T and head dims 64 / 128.
+//
+// Replaces, for that case, the SDPA call of HF's OPTAttention.forward
+// (transformers modeling_opt; reached from the reference's model call in
+// forward_wrap_with_option_len, trainer.py:1464). The inputs are the
+// projections as the fused k/v/q GEMM leaves them: q unscaled (the kernel
+// applies HF's `q * scaling` as R_T(fp32(q) * scaling)), k and v strided
+// views of the same buffer. Output: (sequences, L, heads, head_dim), the
+// layout HF's attention returns before its reshape.
+//
+// One 256-thread workgroup per (sequence, head). V is staged transposed in
+// LDS; each wave takes 32-query blocks and walks the key tiles at or below
+// the diagonal with an online softmax:
+//   S^T (32 keys x 32 queries) = K_tile . Q^T      v_mfma_f32_32x32x16_{f16,bf16}
+//   O^T (32 dims x 32 queries) += V^T_tile . P^T
+// Computing the transposed products puts one query in each lane (and its
+// lane ^ 32 partner), so the running max, the sum and the rescale of O are
+// per-lane values, and the S^T accumulator's slots 8c..8c+7 are already the
+// B operand of the P^T product over keys 16c..16c+15 of the tile (the V^T
+// operand is read with the same key order). P is rounded to T before the
+// second product, as flash attention does; softmax and accumulation are fp32.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dz_common.h"
+#include "dz_kernels.h"
+
+namespace dz {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(1))) u32x4_t g_u32x4_t;
+
+constexpr float kLog2e = 1.4426950408889634f;  // 1 / ln 2
+
+template <int DT>
+struct AttnT;
+template <>
+struct AttnT<DZ_F16> {
+  __device__ static __forceinline__ float to_f(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  }
+  __device__ static __forceinline__ uint32_t from_f(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+  __device__ static __forceinline__ f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
+                                                  0, 0, 0);
+  }
+};
+template <>
+struct AttnT<DZ_BF16> {
+  __device__ static __forceinline__ float to_f(uint32_t h) { return __uint_as_float(h << 16); }
+  __device__ static __forceinline__ uint32_t from_f(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+  }
+  __device__ static __forceinline__ f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8_t, a), __builtin_bit_cast(bf8_t, b), c, 0,
+                                                   0, 0);
+  }
+};
+
+__device__ __forceinline__ u32x4_t ld16(const uint16_t* p) { return *(const g_u32x4_t*)(uintptr_t)p; }
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return AttnT<DT>::from_f(lo) | (AttnT<DT>::from_f(hi) << 16);
+}
+
+// One 32-query block of one (sequence, head).
+template <int DT, int HD>
+__device__ __forceinline__ void attn_block(const AttnArgs& a, const uint16_t* vt, int ldr, int64_t seq, int head,
+                                           int qb) {
+  constexpr int KK = HD / 16;  // MFMA k-steps over the head dim
+  constexpr int DTL = HD / 32;  // 32-dim tiles of O^T
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 31, hf = lane >> 5;
+  const int q0 = 32 * qb;
+
+  // Q^T as B operands: lane holds query q0 + n, dims 16 kk + 8 hf + 0..7, scaled as HF scales q.
+  u32x4_t bq[KK];
+  {
+    const uint16_t* qrow = a.q + seq * a.q_seq + (int64_t)(q0 + n) * a.q_tok + head * HD + 8 * hf;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const u32x4_t x = ld16(qrow + 16 * kk);
+      u32x4_t y;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        y[j] = pack2<DT>(AttnT<DT>::to_f(x[j] & 0xffffu) * a.scale, AttnT<DT>::to_f(x[j] >> 16) * a.scale);
+      }
+      bq[kk] = y;
+    }
+  }
+
+  f32x16_t acc[DTL];
+#pragma unroll
+  for (int t = 0; t < DTL; ++t) acc[t] = f32x16_t{};
+  float m = -__builtin_inff();
+  float lsum = 0.0f;
+  const uint16_t* kbase = a.k + seq * a.k_seq + head * HD + 8 * hf;
+
+  for (int kt = 0; kt <= qb; ++kt) {
+    const int k0 = 32 * kt;
+    // S^T: lane's A row is key k0 + n
+    const uint16_t* krow = kbase + (int64_t)(k0 + n) * a.k_tok;
+    u32x4_t ak[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) ak[kk] = ld16(krow + 16 * kk);
+    f32x16_t s = f32x16_t{};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) s = AttnT<DT>::mfma(ak[kk], bq[kk], s);
+    // s[i] = S^T[key k0 + 8 (i / 4) + 4 hf + i % 4][query q0 + n]
+    if (kt == qb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (8 * (i >> 2) + 4 * hf + (i & 3) > n) s[i] = -__builtin_inff();
+      }
+    }
+    float mx = s[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mnew = fmaxf(m, mx);
+    const float corr = __builtin_amdgcn_exp2f((m - mnew) * kLog2e);
+    const float mb = mnew * kLog2e;
+    float p[16];
+    float ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      p[i] = __builtin_amdgcn_exp2f(s[i] * kLog2e - mb);
+      ps += p[i];
+    }
+    ps += __shfl_xor(ps, 32);
+    lsum = lsum * corr + ps;
+    m = mnew;
+    u32x4_t bp[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bp[c][j] = pack2<DT>(p[8 * c + 2 * j], p[8 * c + 2 * j + 1]);
+    }
+#pragma unroll
+    for (int t = 0; t < DTL; ++t) {
+      acc[t] *= corr;
+      // A row = dim 32 t + n; slots 0..3 / 4..7 = keys k0 + 16 c + 4 hf + 0..3 / + 8 + 0..3
+      const uint16_t* vr = vt + (32 * t + n) * ldr + k0 + 4 * hf;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const u32x2_t lo = *(const u32x2_t*)(vr + 16 * c);
+        const u32x2_t hi = *(const u32x2_t*)(vr + 16 * c + 8);
+        const u32x4_t av = {lo[0], lo[1], hi[0], hi[1]};
+        acc[t] = AttnT<DT>::mfma(av, bp[c], acc[t]);
+      }
+    }
+  }
+
+  // O[query q0 + n][dim 32 t + 8 g + 4 hf + 0..3] = acc[t][4 g + 0..3] / lsum
+  const float inv = 1.0f / lsum;
+  uint16_t* orow = a.out + ((seq * a.L + q0 + n) * (int64_t)a.H + head) * HD + 4 * hf;
+#pragma unroll
+  for (int t = 0; t < DTL; ++t) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      u32x2_t w;
+      w[0] = pack2<DT>(acc[t][4 * g] * inv, acc[t][4 * g + 1] * inv);
+      w[1] = pack2<DT>(acc[t][4 * g + 2] * inv, acc[t][4 * g + 3] * inv);
+      *(u32x2_t*)(orow + 32 * t + 8 * g) = w;
+    }
+  }
+}
+
+template <int DT, int HD>
+__global__ __launch_bounds__(256) void attn_causal_kernel(AttnArgs a) {
+  extern __shared__ uint16_t vt[];  // HD rows of L + 4 keys: V transposed
+  const int L = a.L;
+  const int ldr = L + 4;
+  const int64_t seq = blockIdx.x / a.H;
+  const int head = blockIdx.x % a.H;
+
+  // Stage V^T: each thread moves 8 dims of one key; consecutive lanes take
+  // consecutive keys, so the transposed 2-byte writes of a wave are contiguous.
+  const uint16_t* vbase = a.v + seq * a.v_seq + head * HD;
+  for (int idx = threadIdx.x; idx < L * (HD / 8); idx += 256) {
+    const int key = idx % L, c = idx / L;
+    const u32x4_t x = ld16(vbase + (int64_t)key * a.v_tok + 8 * c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      vt[(8 * c + 2 * j) * ldr + key] = (uint16_t)(x[j] & 0xffffu);
+      vt[(8 * c + 2 * j + 1) * ldr + key] = (uint16_t)(x[j] >> 16);
+    }
+  }
+  __syncthreads();
+
+  // Query blocks of this wave: with <= 4 blocks one each, rotated across
+  // workgroups (block b has b + 1 key tiles, so a fixed assignment would load
+  // one SIMD with the longest); with more, pairs (p, nqb - 1 - p) of equal total work.
+  const int wave = threadIdx.x >> 6;
+  const int nqb = L / 32;
+  if (nqb <= 4) {
+    if (wave < nqb) attn_block<DT, HD>(a, vt, ldr, seq, head, (int)((wave + blockIdx.x) % nqb));
+  } else {
+    for (int p = wave; p < (nqb + 1) / 2; p += 4) {
+      attn_block<DT, HD>(a, vt, ldr, seq, head, p);
+      if (nqb - 1 - p != p) attn_block<DT, HD>(a, vt, ldr, seq, head, nqb - 1 - p);
+    }
+  }
+}
+
+}  // namespace
+
+size_t attn_lds_bytes(int head_dim, int L) { return (size_t)head_dim * (size_t)(L + 4) * 2; }
+
+// Dynamic LDS above 64 KB (L = 256 at head_dim 128) has to be allowed per
+// kernel; done once per instantiation, for the largest size any call uses.
+template <int DT, int HD>
+hipError_t allow_lds() {
+  static const hipError_t e = hipFuncSetAttribute((const void*)attn_causal_kernel<DT, HD>,
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  (int)attn_lds_bytes(HD, 256));
+  return e;
+}
+
+hipError_t launch_attn_causal(int dtype, int head_dim, const AttnArgs& a, uint32_t nblocks, hipStream_t st) {
+  const size_t lds = attn_lds_bytes(head_dim, a.L);
+#define DZ_ATTN_CASE(DTV, HDV)                                                                    \
+  if (dtype == DTV && head_dim == HDV) {                                                          \
+    const hipError_t e = allow_lds<DTV, HDV>();                                                   \
+    if (e != hipSuccess) return e;                                                                \
+    hipLaunchKernelGGL((attn_causal_kernel<DTV, HDV>), dim3(nblocks), dim3(256), lds, st, a);     \
+    return hipGetLastError();                                                                     \
+  }
+  DZ_ATTN_CASE(DZ_F16, 64)
+  DZ_ATTN_CASE(DZ_F16, 128)
+  DZ_ATTN_CASE(DZ_BF16, 64)
+  DZ_ATTN_CASE(DZ_BF16, 128)
+#undef DZ_ATTN_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace dz

@@ -158,6 +158,21 @@ int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sum
 int32_t dz_group_dot(dz_table* t, const uint64_t* other_ptrs, double* d_dot, float* d_dot_f32,
                      void* stream);
 
+/* Causal self-attention of an unpadded batch, for the ZO step's forwards: the
+ * SDPA call of HF's OPTAttention.forward when no mask is given (is_causal), as
+ * reached from the reference's model call in forward_wrap_with_option_len
+ * (trainer.py:1464). dtype DZ_DTYPE_F16 or DZ_DTYPE_BF16; head_dim 64 or 128;
+ * L a multiple of 32 in [32, 256]. Element offsets: token t of sequence b,
+ * head h of q starts at q + b * q_seq + t * q_tok + h * head_dim (k and v
+ * alike); pointers and strides 16-byte aligned. q is used as R_T(q * scale)
+ * (HF scales q by head_dim^-0.5 in T before the product); softmax and
+ * accumulation in fp32, P rounded to T before the product with V. out:
+ * (n_seq, L, H, head_dim) contiguous, not overlapping q, k or v. */
+int32_t dz_attention_causal(int32_t dtype, const void* q, const void* k, const void* v, void* out,
+                            int64_t q_tok, int64_t k_tok, int64_t v_tok, int64_t q_seq, int64_t k_seq,
+                            int64_t v_seq, int32_t n_seq, int32_t L, int32_t H, int32_t head_dim, float scale,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif
