@@ -42,7 +42,7 @@ def test_fuse_changes_layout_not_names(base):
     vals0 = {k: v.clone() for k, v in b.state_dict().items()}
     got = fuse_forward(b)
     L = SHAPES["opt-tiny"].layers
-    assert got == {"mlp": L, "qkv": L}
+    assert got == {"mlp": L, "qkv": L, "attention": 0}
     assert [n for n, _ in b.named_parameters()] == names0
     assert list(b.state_dict().keys()) == keys0
     for k, v in b.state_dict().items():
@@ -135,7 +135,7 @@ def test_models_of_other_forms_are_left_alone():
                       num_attention_heads=2, num_key_value_heads=1)
     m = LlamaForCausalLM(cfg)
     ptrs = [p.data_ptr() for p in m.parameters()]
-    assert fuse_forward(m) == {"mlp": 0, "qkv": 0}
+    assert fuse_forward(m, attention=True) == {"mlp": 0, "qkv": 0, "attention": 0}
     assert [p.data_ptr() for p in m.parameters()] == ptrs
     gelu = torch.nn.Module()
     gelu.fc1 = torch.nn.Linear(4, 4)
