@@ -163,3 +163,19 @@ def test_trainer_applies_the_fusions(base):
     tr2.args = ZOArguments(learning_rate=1e-3, max_steps=5, enhanced=None)
     tr2.zo_setup(plain)
     assert type(plain.model.decoder.layers[0].self_attn) is not FusedQKVOPTAttention
+
+
+def test_library_attention_flag_falls_back_off_gpu(base):
+    """use_library_attention marks the fused modules only; on the CPU (or for
+    any case the kernel does not take) the forward is SDPA's, unchanged."""
+    from dizo_amd.fused_layers import use_library_attention
+
+    a = copy.deepcopy(base)
+    b = copy.deepcopy(base)
+    assert use_library_attention(b) == 0  # not fused yet: nothing marked
+    assert fuse_forward(b, attention=True)["attention"] == SHAPES["opt-tiny"].layers
+    assert all(layer.self_attn.dz_attention for layer in b.model.decoder.layers)
+    batch = make_batches(1, 2, 512, seed=6, device="cpu", fixed_len=32)[0]
+    assert torch.equal(_bits(_logits(a, batch)), _bits(_logits(b, batch)))
+    assert use_library_attention(b, on=False) == SHAPES["opt-tiny"].layers
+    assert not any(layer.self_attn.dz_attention for layer in b.model.decoder.layers)
