@@ -10,8 +10,11 @@
 // layout HF's attention returns before its reshape.
 //
 // One 256-thread workgroup per (sequence, head). V is staged transposed in
-// LDS; each wave takes 32-query blocks and walks the key tiles at or below
-// the diagonal with an online softmax:
+// LDS, and for L <= 128 K as well (row-major, rows padded by 8 elements), so
+// the key loop reads only LDS; for longer sequences both would not leave room
+// for two workgroups per CU, and K is read from global memory. Each wave
+// takes 32-query blocks and walks the key tiles at or below the diagonal with
+// an online softmax:
 //   S^T (32 keys x 32 queries) = K_tile . Q^T      v_mfma_f32_32x32x16_{f16,bf16}
 //   O^T (32 dims x 32 queries) += V^T_tile . P^T
 // Computing the transposed products puts one query in each lane (and its
@@ -72,10 +75,15 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return AttnT<DT>::from_f(lo) | (AttnT<DT>::from_f(hi) << 16);
 }
 
-// One 32-query block of one (sequence, head).
-template <int DT, int HD>
-__device__ __forceinline__ void attn_block(const AttnArgs& a, const uint16_t* vt, int ldr, int64_t seq, int head,
-                                           int qb) {
+// Row stride of K staged in LDS: 8 elements of padding put the 16-byte
+// operand reads of 16 consecutive rows on distinct banks.
+template <int HD>
+constexpr int kKRow = HD + 8;
+
+// One 32-query block of one (sequence, head); ks is K in LDS when KL.
+template <int DT, int HD, bool KL>
+__device__ __forceinline__ void attn_block(const AttnArgs& a, const uint16_t* vt, const uint16_t* ks, int ldr,
+                                           int64_t seq, int head, int qb) {
   constexpr int KK = HD / 16;  // MFMA k-steps over the head dim
   constexpr int DTL = HD / 32;  // 32-dim tiles of O^T
   const int lane = threadIdx.x & 63;
@@ -108,10 +116,16 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const uint16_t* vt
   for (int kt = 0; kt <= qb; ++kt) {
     const int k0 = 32 * kt;
     // S^T: lane's A row is key k0 + n
-    const uint16_t* krow = kbase + (int64_t)(k0 + n) * a.k_tok;
     u32x4_t ak[KK];
+    if constexpr (KL) {
+      const uint16_t* krow = ks + (k0 + n) * kKRow<HD> + 8 * hf;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) ak[kk] = ld16(krow + 16 * kk);
+      for (int kk = 0; kk < KK; ++kk) ak[kk] = *(const u32x4_t*)(krow + 16 * kk);
+    } else {
+      const uint16_t* krow = kbase + (int64_t)(k0 + n) * a.k_tok;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) ak[kk] = ld16(krow + 16 * kk);
+    }
     f32x16_t s = f32x16_t{};
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) s = AttnT<DT>::mfma(ak[kk], bq[kk], s);
@@ -175,24 +189,38 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const uint16_t* vt
   }
 }
 
-template <int DT, int HD>
+template <int DT, int HD, bool KL>
 __global__ __launch_bounds__(256) void attn_causal_kernel(AttnArgs a) {
-  extern __shared__ uint16_t vt[];  // HD rows of L + 4 keys: V transposed
+  // HD rows of L + 4 keys: V transposed; then, when KL, L rows of K
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* vt = smem;
   const int L = a.L;
   const int ldr = L + 4;
+  uint16_t* ks = smem + HD * ldr;
   const int64_t seq = blockIdx.x / a.H;
   const int head = blockIdx.x % a.H;
 
-  // Stage V^T: each thread moves 8 dims of one key; consecutive lanes take
-  // consecutive keys, so the transposed 2-byte writes of a wave are contiguous.
+  // Stage V^T: each thread moves 8 dims of two consecutive keys and writes
+  // each dim's pair of keys as one 32-bit word; consecutive lanes take
+  // consecutive key pairs, so a wave's writes to one row are contiguous.
   const uint16_t* vbase = a.v + seq * a.v_seq + head * HD;
-  for (int idx = threadIdx.x; idx < L * (HD / 8); idx += 256) {
-    const int key = idx % L, c = idx / L;
-    const u32x4_t x = ld16(vbase + (int64_t)key * a.v_tok + 8 * c);
+  uint32_t* vt32 = (uint32_t*)vt;
+  for (int idx = threadIdx.x; idx < (L / 2) * (HD / 8); idx += 256) {
+    const int kp = idx % (L / 2), c = idx / (L / 2);
+    const u32x4_t x0 = ld16(vbase + (int64_t)(2 * kp) * a.v_tok + 8 * c);
+    const u32x4_t x1 = ld16(vbase + (int64_t)(2 * kp + 1) * a.v_tok + 8 * c);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      vt[(8 * c + 2 * j) * ldr + key] = (uint16_t)(x[j] & 0xffffu);
-      vt[(8 * c + 2 * j + 1) * ldr + key] = (uint16_t)(x[j] >> 16);
+      vt32[((8 * c + 2 * j) * ldr) / 2 + kp] = (x0[j] & 0xffffu) | (x1[j] << 16);
+      vt32[((8 * c + 2 * j + 1) * ldr) / 2 + kp] = (x0[j] >> 16) | (x1[j] & 0xffff0000u);
+    }
+  }
+  if constexpr (KL) {
+    // K row-major, 16-byte chunks; consecutive lanes take consecutive chunks of a row
+    const uint16_t* kb = a.k + seq * a.k_seq + head * HD;
+    for (int idx = threadIdx.x; idx < L * (HD / 8); idx += 256) {
+      const int key = idx / (HD / 8), c = idx % (HD / 8);
+      *(u32x4_t*)(ks + key * kKRow<HD> + 8 * c) = ld16(kb + (int64_t)key * a.k_tok + 8 * c);
     }
   }
   __syncthreads();
@@ -203,37 +231,49 @@ __global__ __launch_bounds__(256) void attn_causal_kernel(AttnArgs a) {
   const int wave = threadIdx.x >> 6;
   const int nqb = L / 32;
   if (nqb <= 4) {
-    if (wave < nqb) attn_block<DT, HD>(a, vt, ldr, seq, head, (int)((wave + blockIdx.x) % nqb));
+    if (wave < nqb) attn_block<DT, HD, KL>(a, vt, ks, ldr, seq, head, (int)((wave + blockIdx.x) % nqb));
   } else {
     for (int p = wave; p < (nqb + 1) / 2; p += 4) {
-      attn_block<DT, HD>(a, vt, ldr, seq, head, p);
-      if (nqb - 1 - p != p) attn_block<DT, HD>(a, vt, ldr, seq, head, nqb - 1 - p);
+      attn_block<DT, HD, KL>(a, vt, ks, ldr, seq, head, p);
+      if (nqb - 1 - p != p) attn_block<DT, HD, KL>(a, vt, ks, ldr, seq, head, nqb - 1 - p);
     }
   }
 }
 
 }  // namespace
 
-size_t attn_lds_bytes(int head_dim, int L) { return (size_t)head_dim * (size_t)(L + 4) * 2; }
+// K goes to LDS up to this length (both tables then fit twice in a CU's LDS).
+constexpr int kKLdsMaxLen = 128;
 
-// Dynamic LDS above 64 KB (L = 256 at head_dim 128) has to be allowed per
-// kernel; done once per instantiation, for the largest size any call uses.
-template <int DT, int HD>
+size_t attn_lds_bytes(int head_dim, int L) {
+  const size_t v = (size_t)head_dim * (size_t)(L + 4) * 2;
+  return L <= kKLdsMaxLen ? v + (size_t)L * (size_t)(head_dim + 8) * 2 : v;
+}
+
+// Dynamic LDS above 64 KB has to be allowed per kernel; done once per
+// instantiation, for the largest size that instantiation is launched with.
+template <int DT, int HD, bool KL>
 hipError_t allow_lds() {
-  static const hipError_t e = hipFuncSetAttribute((const void*)attn_causal_kernel<DT, HD>,
+  static const hipError_t e = hipFuncSetAttribute((const void*)attn_causal_kernel<DT, HD, KL>,
                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                  (int)attn_lds_bytes(HD, 256));
+                                                  (int)attn_lds_bytes(HD, KL ? kKLdsMaxLen : 256));
   return e;
 }
 
 hipError_t launch_attn_causal(int dtype, int head_dim, const AttnArgs& a, uint32_t nblocks, hipStream_t st) {
   const size_t lds = attn_lds_bytes(head_dim, a.L);
-#define DZ_ATTN_CASE(DTV, HDV)                                                                    \
-  if (dtype == DTV && head_dim == HDV) {                                                          \
-    const hipError_t e = allow_lds<DTV, HDV>();                                                   \
-    if (e != hipSuccess) return e;                                                                \
-    hipLaunchKernelGGL((attn_causal_kernel<DTV, HDV>), dim3(nblocks), dim3(256), lds, st, a);     \
-    return hipGetLastError();                                                                     \
+#define DZ_ATTN_CASE(DTV, HDV)                                                                        \
+  if (dtype == DTV && head_dim == HDV) {                                                              \
+    if (a.L <= kKLdsMaxLen) {                                                                         \
+      const hipError_t e = allow_lds<DTV, HDV, true>();                                               \
+      if (e != hipSuccess) return e;                                                                  \
+      hipLaunchKernelGGL((attn_causal_kernel<DTV, HDV, true>), dim3(nblocks), dim3(256), lds, st, a); \
+    } else {                                                                                          \
+      const hipError_t e = allow_lds<DTV, HDV, false>();                                              \
+      if (e != hipSuccess) return e;                                                                  \
+      hipLaunchKernelGGL((attn_causal_kernel<DTV, HDV, false>), dim3(nblocks), dim3(256), lds, st, a);\
+    }                                                                                                 \
+    return hipGetLastError();                                                                         \
   }
   DZ_ATTN_CASE(DZ_F16, 64)
   DZ_ATTN_CASE(DZ_F16, 128)
