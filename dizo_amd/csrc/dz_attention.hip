@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "dz_common.h"
 #include "dz_kernels.h"
 
@@ -250,13 +252,21 @@ size_t attn_lds_bytes(int head_dim, int L) {
   return L <= kKLdsMaxLen ? v + (size_t)L * (size_t)(head_dim + 8) * 2 : v;
 }
 
-// Dynamic LDS above 64 KB has to be allowed per kernel; done once per
-// instantiation, for the largest size that instantiation is launched with.
+// Dynamic LDS above 64 KB has to be allowed per kernel and device; done once
+// per (instantiation, device), for the largest size the instantiation takes.
 template <int DT, int HD, bool KL>
 hipError_t allow_lds() {
-  static const hipError_t e = hipFuncSetAttribute((const void*)attn_causal_kernel<DT, HD, KL>,
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                  (int)attn_lds_bytes(HD, KL ? kKLdsMaxLen : 256));
+  static std::mutex mu;
+  static uint64_t done = 0;  // bit d: set on device d
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if ((done >> dev) & 1u) return hipSuccess;
+  e = hipFuncSetAttribute((const void*)attn_causal_kernel<DT, HD, KL>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)attn_lds_bytes(HD, KL ? kKLdsMaxLen : 256));
+  if (e == hipSuccess) done |= 1ull << dev;
   return e;
 }
 
