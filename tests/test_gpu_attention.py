@@ -71,6 +71,29 @@ def test_attention_matches_fp32_reference(n_seq, L, H, hd, dt):
     assert err <= 2.0 * err_sdpa + bound / 4
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_attention_large_scores_stay_finite_and_accurate(dt):
+    """q and k of standard deviation 6: scaled scores reach about +-100, far
+    outside exp's range without the running-max subtraction. The output must
+    stay finite and as close to the fp32 reference as SDPA's."""
+    from dizo_amd.attention import attention_causal
+
+    n_seq, L, H, hd = 2, 128, 4, 128
+    kvq = _kvq(n_seq, L, H, hd, dt, seed=21, std=6.0)
+    d = H * hd
+    k, v, q = kvq.split(d, dim=-1)
+    scale = hd ** -0.5
+    out = attention_causal(q, k, v, H, hd, scale)
+    ref, qh, kh, vh = _reference(q, k, v, H, hd, scale)
+    with torch.inference_mode():
+        sdpa = F.scaled_dot_product_attention(qh, kh, vh, is_causal=True, scale=1.0).transpose(1, 2).float()
+    assert bool(torch.isfinite(out).all())
+    err = (out.float() - ref).abs().max().item()
+    err_sdpa = (sdpa - ref).abs().max().item()
+    print(f"[attention large] {dt}: max|out - ref| {err:.3g}, max|sdpa - ref| {err_sdpa:.3g}", flush=True)
+    assert err <= 2.0 * err_sdpa + 1e-3
+
+
 def test_attention_first_query_is_its_value_row():
     """Query 0 sees only key 0: its output is v[0] rounded to T (softmax weight exactly 1)."""
     from dizo_amd.attention import attention_causal
