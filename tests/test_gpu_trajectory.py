@@ -69,14 +69,15 @@ def _ref_forward(model, batch):
         return forward_wrap_with_option_len(model, **batch, return_dict=True).loss.detach()
 
 
-def _library_run(shape, dt, batches, steps, lr0, eps, seed=5, progress=_quiet):
-    """The library trainer (ENHANCED=zo, fused passes). Returns the trainer (kept
-    open for export_z), its losses, its model and a copy of the initial model."""
+def _library_run(shape, dt, batches, steps, lr0, eps, seed=5, progress=_quiet, **zo_args):
+    """The library trainer (ENHANCED=zo, fused passes; zo_args: further
+    ZOArguments). Returns the trainer (kept open for export_z), its losses, its
+    model and a copy of the initial model."""
     from dizo_amd.synth import Cycle, build_opt
     from dizo_amd.trainer import ZOArguments, ZOTrainer
     model = build_opt(shape, dt, "cuda", seed=seed)
     init = copy.deepcopy(model)
-    args = ZOArguments(learning_rate=lr0, zo_eps=eps, max_steps=steps, enhanced="zo")
+    args = ZOArguments(learning_rate=lr0, zo_eps=eps, max_steps=steps, enhanced="zo", **zo_args)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches))
     losses = []
@@ -208,6 +209,30 @@ def test_c3_shape_200_step_loss_trajectory(capsys):
     print(f"C3 vs recipe + torch.norm: {same_c}/200 losses bit-identical, max |dL| = {worst_c:.3g}", flush=True)
     assert worst_c <= 1e-3, f"max loss difference {worst_c} over 200 steps"
     tr.zo_close()
+
+
+def test_c3_shape_fused_forward_bit_identical():
+    """The bench's forward at C3's shape (OPT-2.7B fp16, padded batches of 16 x 2
+    candidates): with the fused decoder-layer GEMMs and the library attention
+    asked for (padded batches keep SDPA), 50 steps with a DiZO event give the
+    losses, gamma and weights of HF's layer code bit for bit."""
+    from dizo_amd.synth import make_batches
+
+    batches = make_batches(8, 16, 50272, seed=3, device="cuda", min_len=32, max_len=64)
+    runs = []
+    for fused in (True, False):
+        tr, la, ma, _ = _library_run("opt-2.7b", torch.float16, batches, 50, 1e-6, 1e-3, zo_fused_mlp=fused,
+                                     zo_fused_qkv=fused, zo_fused_attention=fused, zo_option_head=True)
+        runs.append((tr.dizo_trainer.dizo.gamma(), la, {n: p.detach().clone() for n, p in ma.named_parameters()}))
+        tr.zo_close()
+        del tr, ma
+        torch.cuda.empty_cache()
+    (ga, la, pa), (gb, lb, pb) = runs
+    bad = [k for k, (a, b) in enumerate(zip(la, lb)) if not _same(a, b)]
+    assert not bad, f"losses differ at steps {bad[:5]}"
+    assert _same(ga, gb)
+    diff = [n for n in pa if not _same(pa[n], pb[n])]
+    assert not diff, f"{len(diff)} tensors differ, e.g. {diff[:3]}"
 
 
 def test_c2_opt27b_separate_and_fused_passes():
