@@ -122,6 +122,22 @@ def qkv_views(attn) -> Optional[tuple]:
 # is_causal path): HF's SDPA and the capture-safe registration in dizo_amd.graph
 _SDPA_IMPLS = ("sdpa", "dizo_sdpa")
 
+# (mask, dtype, additive form) of the last boolean mask converted
+_mask_cache: list = [None, None, None]
+
+
+def _additive_mask(mask: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """SDPA's additive form of a boolean mask (0 where attended, -inf
+    elsewhere), made once per mask object: HF passes one mask tensor to every
+    layer of a forward, and SDPA given the boolean one converts it on every
+    call (two fills and a select per layer). SDPA gives the same bits with
+    either form."""
+    if _mask_cache[0] is mask and _mask_cache[1] == dtype:
+        return _mask_cache[2]
+    add = torch.zeros(mask.shape, dtype=dtype, device=mask.device).masked_fill_(~mask, float("-inf"))
+    _mask_cache[:] = [mask, dtype, add]
+    return add
+
 
 class FusedQKVOPTAttention(_opt.OPTAttention):
     """OPTAttention whose three input projections run as one GEMM (module doc)."""
@@ -145,6 +161,9 @@ class FusedQKVOPTAttention(_opt.OPTAttention):
 
             out = attention_causal(q, k, v, self.num_heads, self.head_dim, self.scaling)
             return self.out_proj(out.view(bsz, tgt_len, -1)), None
+        if (attention_mask is not None and attention_mask.dtype == torch.bool
+                and self.config._attn_implementation in _SDPA_IMPLS):
+            attention_mask = _additive_mask(attention_mask, q.dtype)
         # HF's order: q rounded to T by the GEMM, then scaled (one more rounding)
         query_states = (q * self.scaling).view(bsz, -1, self.num_heads, self.head_dim).transpose(1, 2)
         key_states = k.view(bsz, -1, self.num_heads, self.head_dim).transpose(1, 2)
