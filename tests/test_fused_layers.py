@@ -179,3 +179,24 @@ def test_library_attention_flag_falls_back_off_gpu(base):
     assert torch.equal(_bits(_logits(a, batch)), _bits(_logits(b, batch)))
     assert use_library_attention(b, on=False) == SHAPES["opt-tiny"].layers
     assert not any(layer.self_attn.dz_attention for layer in b.model.decoder.layers)
+
+
+@pytest.mark.parametrize("enable_bias,ln_before", [(False, True), (True, False)])
+def test_fusions_on_other_opt_configs(enable_bias, ln_before):
+    """OPT without biases (the k/v/q buffer without a bias buffer; fc1 left as
+    it is, its epilogue form needs the bias) and OPT-350m's post-norm layout:
+    the same logits bit for bit."""
+    from transformers import OPTConfig
+
+    cfg = OPTConfig(vocab_size=512, hidden_size=64, num_hidden_layers=2, ffn_dim=128, num_attention_heads=4,
+                    max_position_embeddings=128, word_embed_proj_dim=64, enable_bias=enable_bias,
+                    do_layer_norm_before=ln_before, pad_token_id=1, dropout=0.0, attention_dropout=0.0)
+    torch.manual_seed(2)
+    a = OPTForCausalLM(cfg).eval()
+    b = copy.deepcopy(a)
+    got = fuse_forward(b, attention=True)
+    assert got["qkv"] == 2 and got["mlp"] == (2 if enable_bias else 0)
+    w, bias = qkv_views(b.model.decoder.layers[0].self_attn)
+    assert (bias is None) == (not enable_bias)
+    batch = make_batches(1, 3, 512, seed=4, device="cpu", min_len=6, max_len=20)[0]
+    assert torch.equal(_bits(_logits(a, batch)), _bits(_logits(b, batch)))
