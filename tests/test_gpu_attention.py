@@ -218,3 +218,35 @@ def test_graph_replays_library_attention_bit_identical():
     pb = dict(b.named_parameters())
     for n, p in a.named_parameters():
         assert torch.equal(p, pb[n]), n
+
+
+def test_graph_with_fused_forward_across_dizo_event_bit_identical():
+    """50 steps with a DiZO event (its projection table built over the k/v
+    weights after they moved into the fused buffer): captured-graph steps and
+    eager steps, both with the fused forward and the library attention, give
+    the same losses, gamma and weights bit for bit."""
+    import copy
+
+    import numpy as np
+
+    from dizo_amd.synth import Cycle, make_batches
+    from dizo_amd.trainer import ZOArguments, ZOTrainer
+
+    a = _mini(torch.float16, seed=7)
+    b = copy.deepcopy(a)
+    batches = make_batches(50, 4, 4096, seed=10, device="cuda", fixed_len=64)
+    out = []
+    for model, graph in ((a, True), (b, False)):
+        np.random.seed(14)
+        args = ZOArguments(learning_rate=1e-4, zo_eps=1e-3, max_steps=50, enhanced="zo", zo_fused_mlp=True,
+                           zo_fused_qkv=True, zo_fused_attention=True, zo_graph=graph, zo_option_head=True)
+        tr = ZOTrainer(model, args, train_dataloader=Cycle(batches[:6]))
+        losses = torch.stack([tr.training_step(x).clone() for x in batches])
+        tr.zo_flush()
+        out.append((losses, tr.dizo_trainer.dizo.gamma().clone()))
+        tr.zo_close()
+    assert torch.equal(out[0][0], out[1][0])
+    assert torch.equal(out[0][1], out[1][1])
+    pb = dict(b.named_parameters())
+    for n, p in a.named_parameters():
+        assert torch.equal(p, pb[n]), n
