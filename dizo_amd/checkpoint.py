@@ -293,12 +293,15 @@ def save_checkpoint(trainer, path: str) -> None:
 
     trainer.zo_flush()
     os.makedirs(path, exist_ok=True)
-    tensors = {n: p.detach().contiguous().cpu() for n, p in trainer.model.named_parameters()}
+    # copies, never views: parameters may share one storage (the fused k/v/q
+    # buffer of dizo_amd.fused_layers), which safetensors refuses, and .cpu()
+    # of a CPU tensor would return the tensor itself
+    tensors = {n: p.detach().to("cpu", copy=True).contiguous() for n, p in trainer.model.named_parameters()}
     dtr = getattr(trainer, "dizo_trainer", None) if trainer.args.enhanced else None
     if dtr is not None:
         anchors = dict(trainer.base_model.named_parameters())
         for n in dtr.dizo.constraints_name:
-            tensors["anchor:" + n] = anchors[n].detach().contiguous().cpu()
+            tensors["anchor:" + n] = anchors[n].detach().to("cpu", copy=True).contiguous()
     # each file is written to a temporary name and renamed into place, so an
     # interrupted save never leaves a partial file beside an older state
     tmp = os.path.join(path, "theta.safetensors.tmp")

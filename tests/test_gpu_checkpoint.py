@@ -28,13 +28,13 @@ def _batches():
     return make_batches(5, 4, 512, seed=61, device="cuda", min_len=8, max_len=20)
 
 
-def _trainer(dt, enhanced, graph=False, journal=True, seed=71):
+def _trainer(dt, enhanced, graph=False, journal=True, seed=71, fused=False):
     from dizo_amd.synth import Cycle, build_opt
     from dizo_amd.trainer import ZOArguments, ZOTrainer
     model = build_opt("opt-tiny", dt, "cuda", seed=seed)
     init = copy.deepcopy(model)
     args = ZOArguments(learning_rate=1e-3, zo_eps=1e-3, max_steps=120, enhanced=enhanced, zo_graph=graph,
-                       zo_journal=journal)
+                       zo_journal=journal, zo_fused_mlp=fused, zo_fused_qkv=fused, zo_fused_attention=fused)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(_batches()))
     return tr, model, init
@@ -86,15 +86,17 @@ def test_replay_reproduces_the_run(dt, enhanced, graph, tmp_path):
         assert changed > 0
 
 
-@pytest.mark.parametrize("enhanced", ["zo", "fo"])
-def test_resume_from_checkpoint_is_exact(enhanced, tmp_path):
+@pytest.mark.parametrize("enhanced,fused", [("zo", False), ("fo", False), ("zo", True)])
+def test_resume_from_checkpoint_is_exact(enhanced, fused, tmp_path):
     """110 steps uninterrupted against 60 steps, a checkpoint, and a fresh
     trainer that loads it and runs the last 50 (DiZO events at global steps 49
-    and 99, so the second event depends on restored state)."""
+    and 99, so the second event depends on restored state). fused: the
+    decoder layers in the fused forms, whose k/v/q weights share one storage
+    (saved as separate tensors, loaded back in place)."""
     from dizo_amd.checkpoint import load_checkpoint, replay, save_checkpoint
     from dizo_amd.synth import Cycle
     dt = torch.float16
-    tr_a, model_a, init = _trainer(dt, enhanced)
+    tr_a, model_a, init = _trainer(dt, enhanced, fused=fused)
     it = iter(Cycle(_batches()))
     _run(tr_a, it, 60)
     save_checkpoint(tr_a, str(tmp_path / "ckpt"))
@@ -102,7 +104,7 @@ def test_resume_from_checkpoint_is_exact(enhanced, tmp_path):
     gamma_a = tr_a.dizo_trainer.dizo.gamma().clone()
     tr_a.zo_close()
 
-    tr_b, model_b, _ = _trainer(dt, enhanced, seed=99)  # different initial weights: all come from the checkpoint
+    tr_b, model_b, _ = _trainer(dt, enhanced, seed=99, fused=fused)  # different initial weights: all come from the checkpoint
     np.random.seed(1)  # and a different seed stream: it comes from the checkpoint too
     load_checkpoint(tr_b, str(tmp_path / "ckpt"))
     assert tr_b.state.global_step == 60
