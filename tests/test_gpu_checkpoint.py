@@ -86,7 +86,7 @@ def test_replay_reproduces_the_run(dt, enhanced, graph, tmp_path):
         assert changed > 0
 
 
-@pytest.mark.parametrize("enhanced,fused", [("zo", False), ("fo", False), ("zo", True)])
+@pytest.mark.parametrize("enhanced,fused", [("zo", False), ("fo", False), ("zo", True), ("fo", True)])
 def test_resume_from_checkpoint_is_exact(enhanced, fused, tmp_path):
     """110 steps uninterrupted against 60 steps, a checkpoint, and a fresh
     trainer that loads it and runs the last 50 (DiZO events at global steps 49
