@@ -1,9 +1,13 @@
-"""Two GEMM fusions in HF's OPT decoder layer for the ZO step's forwards.
+"""Faster forms of HF's OPT decoder layer for the ZO step's forwards.
 
 The ZO step runs two forwards per step (and 20 per DiZO event) without
 autograd, and at OPT-13B those forwards are ~90 % of the step. Two changes to
 how the layer calls its GEMMs make them cheaper and leave every value as HF's
-layer computes it on this stack.
+layer computes it on this stack; the fused attention module also hands an
+unpadded batch's causal attention to the library's kernel when asked
+(`use_library_attention`, dizo_amd.attention; not bit-identical to SDPA), and
+gives SDPA a padded batch's mask in additive form, made once per forward
+(`_additive_mask`; the same bits).
 
 1. fc1 + ReLU (`OPTDecoderLayer.forward`: `fc2(activation_fn(fc1(h)))`, ReLU
    for every OPT size) as one hipBLASLt call with a bias+ReLU epilogue
