@@ -269,6 +269,34 @@ def kernel_microbench(wl_name: str, reps: int = 10, log=print):
         log(f"[kernels] {name:15s} {t:8.3f} ms {nb / t / 1e6:8.1f} GB/s")
     ptab.close()
     del t0
+    # the forward's causal attention kernel at the workload's batch shape (unpadded batches only): q, k, v
+    # as the fused k/v/q GEMM leaves them; algorithmic bytes = q, k, v read + output written
+    from dizo_amd.attention import attention_causal, supported
+
+    shape = SHAPES[wl["shape"]]
+    hd = shape.d_model // shape.heads
+    Lq = wl["fixed_len"]
+    if Lq:
+        n_seq, d = 2 * wl["batch"], shape.d_model
+        kvq = torch.randn(n_seq, Lq, 3 * d, device="cuda", dtype=torch.float32).to(dtype)
+        k, v, q = kvq.split(d, dim=-1)
+        if supported(q, Lq, hd):
+            fn = lambda: attention_causal(q, k, v, shape.heads, hd, hd ** -0.5)  # noqa: E731
+            fn()
+            torch.cuda.synchronize()
+            ms = []
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                fn()
+                e1.record()
+                torch.cuda.synchronize()
+                ms.append(e0.elapsed_time(e1))
+            t = float(np.median(ms))
+            nb = 4 * n_seq * Lq * d * kvq.element_size()
+            out["attention"] = {"ms": t, "GBps": nb / t / 1e6, "frac": nb / t / 1e6 / HBM_PEAK_GBPS, "bytes": nb}
+            log(f"[kernels] {'attention':15s} {t:8.3f} ms {nb / t / 1e6:8.1f} GB/s")
+        del kvq, k, v, q
     # calibration for counter-based traffic: a plain device copy of known size
     # (reads and writes copy_bytes each), launched twice
     copy_bytes = 4 << 30
