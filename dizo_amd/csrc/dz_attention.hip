@@ -77,10 +77,94 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return AttnT<DT>::from_f(lo) | (AttnT<DT>::from_f(hi) << 16);
 }
 
+// K goes to LDS up to this length (both tables then fit twice in a CU's LDS).
+constexpr int kKLdsMaxLen = 128;
+
 // Row stride of K staged in LDS: 8 elements of padding put the 16-byte
 // operand reads of 16 consecutive rows on distinct banks.
 template <int HD>
 constexpr int kKRow = HD + 8;
+
+__device__ __forceinline__ float max16(const f32x16_t& v) {
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = fmaxf(v[i], v[i + 8]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = fmaxf(a[i], a[i + 4]);
+  return fmaxf(fmaxf(a[0], a[2]), fmaxf(a[1], a[3]));
+}
+
+__device__ __forceinline__ float sum16(const f32x16_t& v) {
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = v[i] + v[i + 8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = a[i] + a[i + 4];
+  return (a[0] + a[2]) + (a[1] + a[3]);
+}
+
+// S^T tile (32 keys k0.. x 32 queries): lane's A row is key k0 + n, read
+// from LDS (ks) or global memory (krow_g); two independent accumulation
+// chains (even and odd k-steps) halve the dependent MFMA latency. Keys above
+// the query are masked on the diagonal tile. Slot i of the result is key
+// k0 + 8 (i / 4) + 4 hf + i % 4.
+template <int DT, int HD, bool KL>
+__device__ __forceinline__ f32x16_t score_tile(const u32x4_t* bq, const uint16_t* ks, const uint16_t* kbase,
+                                               int64_t k_tok, int k0, int n, int hf, bool diag) {
+  constexpr int KK = HD / 16;
+  u32x4_t ak[KK];
+  if constexpr (KL) {
+    const uint16_t* krow = ks + (k0 + n) * kKRow<HD> + 8 * hf;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) ak[kk] = *(const u32x4_t*)(krow + 16 * kk);
+  } else {
+    const uint16_t* krow = kbase + (int64_t)(k0 + n) * k_tok;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) ak[kk] = ld16(krow + 16 * kk);
+  }
+  f32x16_t s0 = f32x16_t{}, s1 = f32x16_t{};
+#pragma unroll
+  for (int kk = 0; kk < KK; kk += 2) {
+    s0 = AttnT<DT>::mfma(ak[kk], bq[kk], s0);
+    if (kk + 1 < KK) s1 = AttnT<DT>::mfma(ak[kk + 1], bq[kk + 1], s1);
+  }
+  f32x16_t st = s0 + s1;
+  if (diag) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (8 * (i >> 2) + 4 * hf + (i & 3) > n) st[i] = -__builtin_inff();
+    }
+  }
+  return st;
+}
+
+// O^T += V^T P^T over the 32 keys k0.. of a tile: p holds this lane's 16 P
+// values (query n, keys k0 + 8 (i / 4) + 4 hf + i % 4), rounded to T here;
+// slots 8c..8c+7 are the B operand over keys k0 + 16c .. +15, and the V^T
+// operand (A row = dim 32 t + n) is read in the same key order.
+template <int DT, int HD>
+__device__ __forceinline__ void pv_tile(f32x16_t* acc, const f32x16_t& p, const uint16_t* vt, int ldr, int k0,
+                                        int n, int hf) {
+  constexpr int DTL = HD / 32;
+  u32x4_t bp[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bp[c][j] = pack2<DT>(p[8 * c + 2 * j], p[8 * c + 2 * j + 1]);
+  }
+#pragma unroll
+  for (int t = 0; t < DTL; ++t) {
+    // slots 0..3 / 4..7 = keys k0 + 16 c + 4 hf + 0..3 / + 8 + 0..3
+    const uint16_t* vr = vt + (32 * t + n) * ldr + k0 + 4 * hf;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const u32x2_t lo = *(const u32x2_t*)(vr + 16 * c);
+      const u32x2_t hi = *(const u32x2_t*)(vr + 16 * c + 8);
+      const u32x4_t av = {lo[0], lo[1], hi[0], hi[1]};
+      acc[t] = AttnT<DT>::mfma(av, bp[c], acc[t]);
+    }
+  }
+}
 
 // One 32-query block of one (sequence, head); ks is K in LDS when KL.
 template <int DT, int HD, bool KL>
@@ -111,68 +195,58 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const uint16_t* vt
   f32x16_t acc[DTL];
 #pragma unroll
   for (int t = 0; t < DTL; ++t) acc[t] = f32x16_t{};
-  float m = -__builtin_inff();
-  float lsum = 0.0f;
   const uint16_t* kbase = a.k + seq * a.k_seq + head * HD + 8 * hf;
-
-  for (int kt = 0; kt <= qb; ++kt) {
-    const int k0 = 32 * kt;
-    // S^T: lane's A row is key k0 + n
-    u32x4_t ak[KK];
-    if constexpr (KL) {
-      const uint16_t* krow = ks + (k0 + n) * kKRow<HD> + 8 * hf;
+  float lsum;
+  if constexpr (KL) {
+    // At most kKLdsMaxLen / 32 key tiles: a block's scores all fit in
+    // registers, so the softmax takes two passes (the scores and their max,
+    // then P and the products with V) and never rescales the accumulators,
+    // which live in AGPRs.
+    constexpr int kMaxT = kKLdsMaxLen / 32;
+    f32x16_t sc[kMaxT];
+    float m = -__builtin_inff();
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) ak[kk] = *(const u32x4_t*)(krow + 16 * kk);
-    } else {
-      const uint16_t* krow = kbase + (int64_t)(k0 + n) * a.k_tok;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) ak[kk] = ld16(krow + 16 * kk);
-    }
-    f32x16_t s = f32x16_t{};
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) s = AttnT<DT>::mfma(ak[kk], bq[kk], s);
-    // s[i] = S^T[key k0 + 8 (i / 4) + 4 hf + i % 4][query q0 + n]
-    if (kt == qb) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        if (8 * (i >> 2) + 4 * hf + (i & 3) > n) s[i] = -__builtin_inff();
+    for (int kt = 0; kt < kMaxT; ++kt) {
+      if (kt <= qb) {
+        sc[kt] = score_tile<DT, HD, KL>(bq, ks, kbase, a.k_tok, 32 * kt, n, hf, kt == qb);
+        m = fmaxf(m, max16(sc[kt]));
       }
     }
-    float mx = s[0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mnew = fmaxf(m, mx);
-    const float corr = __builtin_amdgcn_exp2f((m - mnew) * kLog2e);
-    const float mb = mnew * kLog2e;
-    float p[16];
+    m = fmaxf(m, __shfl_xor(m, 32));
+    const float mb = m * kLog2e;
     float ps = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      p[i] = __builtin_amdgcn_exp2f(s[i] * kLog2e - mb);
-      ps += p[i];
-    }
-    ps += __shfl_xor(ps, 32);
-    lsum = lsum * corr + ps;
-    m = mnew;
-    u32x4_t bp[2];
+    for (int kt = 0; kt < kMaxT; ++kt) {
+      if (kt <= qb) {
+        f32x16_t p;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bp[c][j] = pack2<DT>(p[8 * c + 2 * j], p[8 * c + 2 * j + 1]);
-    }
-#pragma unroll
-    for (int t = 0; t < DTL; ++t) {
-      acc[t] *= corr;
-      // A row = dim 32 t + n; slots 0..3 / 4..7 = keys k0 + 16 c + 4 hf + 0..3 / + 8 + 0..3
-      const uint16_t* vr = vt + (32 * t + n) * ldr + k0 + 4 * hf;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const u32x2_t lo = *(const u32x2_t*)(vr + 16 * c);
-        const u32x2_t hi = *(const u32x2_t*)(vr + 16 * c + 8);
-        const u32x4_t av = {lo[0], lo[1], hi[0], hi[1]};
-        acc[t] = AttnT<DT>::mfma(av, bp[c], acc[t]);
+        for (int i = 0; i < 16; ++i) p[i] = __builtin_amdgcn_exp2f(sc[kt][i] * kLog2e - mb);
+        ps += sum16(p);
+        pv_tile<DT, HD>(acc, p, vt, ldr, 32 * kt, n, hf);
       }
+    }
+    lsum = ps + __shfl_xor(ps, 32);
+  } else {
+    // Longer sequences: online softmax, one key tile at a time.
+    float m = -__builtin_inff();
+    lsum = 0.0f;
+    for (int kt = 0; kt <= qb; ++kt) {
+      const f32x16_t st = score_tile<DT, HD, KL>(bq, ks, kbase, a.k_tok, 32 * kt, n, hf, kt == qb);
+      float mx = max16(st);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(m, mx);
+      const float corr = __builtin_amdgcn_exp2f((m - mnew) * kLog2e);
+      const float mb = mnew * kLog2e;
+      f32x16_t p;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) p[i] = __builtin_amdgcn_exp2f(st[i] * kLog2e - mb);
+      float ps = sum16(p);
+      ps += __shfl_xor(ps, 32);
+      lsum = lsum * corr + ps;
+      m = mnew;
+#pragma unroll
+      for (int t = 0; t < DTL; ++t) acc[t] *= corr;
+      pv_tile<DT, HD>(acc, p, vt, ldr, 32 * kt, n, hf);
     }
   }
 
@@ -191,8 +265,9 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const uint16_t* vt
   }
 }
 
+// Two waves per SIMD (two workgroups per CU, as the LDS allows).
 template <int DT, int HD, bool KL>
-__global__ __launch_bounds__(256) void attn_causal_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_causal_kernel(AttnArgs a) {
   // HD rows of L + 4 keys: V transposed; then, when KL, L rows of K
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   uint16_t* vt = smem;
@@ -243,9 +318,6 @@ __global__ __launch_bounds__(256) void attn_causal_kernel(AttnArgs a) {
 }
 
 }  // namespace
-
-// K goes to LDS up to this length (both tables then fit twice in a CU's LDS).
-constexpr int kKLdsMaxLen = 128;
 
 size_t attn_lds_bytes(int head_dim, int L) {
   const size_t v = (size_t)head_dim * (size_t)(L + 4) * 2;
