@@ -13,12 +13,13 @@
 // LDS, and for L <= 128 K as well (row-major, rows padded by 8 elements), so
 // the key loop reads only LDS; for longer sequences both would not leave room
 // for two workgroups per CU, and K is read from global memory. Each wave
-// takes 32-query blocks and walks the key tiles at or below the diagonal with
-// an online softmax:
+// takes 32-query blocks and walks the key tiles at or below the diagonal:
 //   S^T (32 keys x 32 queries) = K_tile . Q^T      v_mfma_f32_32x32x16_{f16,bf16}
 //   O^T (32 dims x 32 queries) += V^T_tile . P^T
+// with the softmax in two passes (all scores of a block in registers, then P)
+// for L <= 128 and online (running max, rescaled O) for longer sequences.
 // Computing the transposed products puts one query in each lane (and its
-// lane ^ 32 partner), so the running max, the sum and the rescale of O are
+// lane ^ 32 partner), so the max, the sum and any rescale of O are
 // per-lane values, and the S^T accumulator's slots 8c..8c+7 are already the
 // B operand of the P^T product over keys 16c..16c+15 of the tile (the V^T
 // operand is read with the same key order). P is rounded to T before the
