@@ -394,7 +394,9 @@ def main(argv=None):
                    "graph": a.graph, "option_head": not a.full_logits, "fused_gemms": not a.hf_layers,
                    "attention": "sdpa" if (a.hf_layers or a.sdpa) else "dz_attention_causal (unpadded batches)",
                    "enhanced": a.enhanced,
-                   "seq_len": wl["fixed_len"] or wl["max_len"]},
+                   "seq_len": wl["fixed_len"] or wl["max_len"],
+                   "device": {"name": torch.cuda.get_device_name(0),
+                              "compute_units": torch.cuda.get_device_properties(0).multi_processor_count}},
         "roofline": {
             "kernel": "rmw_kernel (perturb -2 / restore+update / restore+update+next perturb)",
             "bound": "hbm",
