@@ -187,7 +187,9 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const uint16_t* vt
       u32x4_t y;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        y[j] = pack2<DT>(AttnT<DT>::to_f(x[j] & 0xffffu) * a.scale, AttnT<DT>::to_f(x[j] >> 16) * a.scale);
+        // dz_opq: the fp32 product is rounded to T on its own, as HF's `q * scaling` is
+        y[j] = pack2<DT>(dz_opq(AttnT<DT>::to_f(x[j] & 0xffffu) * a.scale),
+                         dz_opq(AttnT<DT>::to_f(x[j] >> 16) * a.scale));
       }
       bq[kk] = y;
     }
@@ -259,8 +261,8 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, const uint16_t* vt
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       u32x2_t w;
-      w[0] = pack2<DT>(acc[t][4 * g] * inv, acc[t][4 * g + 1] * inv);
-      w[1] = pack2<DT>(acc[t][4 * g + 2] * inv, acc[t][4 * g + 3] * inv);
+      w[0] = pack2<DT>(dz_opq(acc[t][4 * g] * inv), dz_opq(acc[t][4 * g + 1] * inv));
+      w[1] = pack2<DT>(dz_opq(acc[t][4 * g + 2] * inv), dz_opq(acc[t][4 * g + 3] * inv));
       *(u32x2_t*)(orow + 32 * t + 8 * g) = w;
     }
   }

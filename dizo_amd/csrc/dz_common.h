@@ -31,6 +31,17 @@
 #define DZ_HD static inline
 #endif
 
+#if defined(__HIPCC__) || defined(__HIP__)
+// Opaque identity: the value must exist as a plain fp32 register here. Placed
+// between an fp32 product and its conversion to a 16-bit type, it keeps the
+// backend from folding the two into one mixed-precision FMA (which rounds the
+// exact product once instead of twice, as PyTorch does).
+__device__ __forceinline__ float dz_opq(float x) {
+  asm("" : "+v"(x));
+  return x;
+}
+#endif
+
 enum DzDtype : int32_t { DZ_F32 = 0, DZ_F16 = 1, DZ_BF16 = 2 };
 
 // Stream ids of the Philox counter word 2.

@@ -19,12 +19,6 @@
 
 namespace dz {
 
-// Opaque identity: the value must exist as a plain fp32 register here.
-__device__ __forceinline__ float dz_opq(float x) {
-  asm("" : "+v"(x));
-  return x;
-}
-
 template <int DT>
 struct DT_;
 
