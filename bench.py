@@ -6,26 +6,35 @@ forward, perturb -2, forward, fused restore+update, and every 50 steps the
 DiZO projection event with 10 SPSA iterations on gamma) on the OPT-13B fp16
 workload (config C4: 40 layers, d_model 5120, batch 16 examples x 2 candidates
 of 128 random tokens, theta0 anchor resident in HBM), synthetic random-init
-weights and synthetic token batches already resident in HBM. The loss's
-forward computes logits only at the option positions the classification loss
-reads (HF's logits_to_keep; the same loss); --full-logits computes them at
-every position as the reference does. Each decoder layer's fc1 + ReLU runs as
-one GEMM with a ReLU epilogue and its k/v/q projections as one GEMM (values
-bit-identical to HF's layer at the C3 and C4 shapes; at C5's the fused k/v/q
-GEMM runs another hipBLASLt kernel and can differ in the last bit);
---hf-layers runs HF's layer code as it is. With the fused layers, an
-unpadded batch's causal attention runs through the library's MFMA kernel
-(dz_attention_causal, q scaling included; not bit-identical to SDPA, within
-its rounding); --sdpa keeps SDPA.
+weights and synthetic token batches already resident in HBM.
+
+Every timed window holds at least one DiZO event: the trainer's step counter
+starts where the event (after the update of every 50th step,
+trainer.py:1611) falls on the window's last step (on steps 49, 99, ... of the
+window when --steps exceeds 50). `value` is the amortised rate, one event per
+50 steps: steps / (t_steps + t_event * steps / 50), with t_event the mean
+timed event and t_steps the window's time without its events; the plain ZO
+step rate and the event time are reported beside it.
+
+The forward stays on PyTorch-ROCm: SDPA's attention and HF's decoder layers,
+with two GEMM-level fusions that give HF's values bit for bit at the bench
+shapes (fc1 + ReLU as one GEMM with a ReLU epilogue; k/v/q as one GEMM), and
+logits computed only at the option positions the classification loss reads
+(HF's logits_to_keep; the same loss). --full-logits computes them at every
+position as the reference does; --hf-layers runs HF's layer code as it is;
+--dz-attention sends an unpadded batch's causal attention through the
+library's MFMA kernel (dz_attention_causal; within SDPA's rounding, not bit
+for bit, so its loss trajectory drifts from SDPA's: opt-in).
 
 Prints one JSON line. `roofline` is the dominant library kernel (the
 multi-tensor perturb / restore+update read-modify-write): algorithmic bytes
 2*b*P per launch over its mean device time, measured with stream events
 around every launch in the timed region. `cpu_baseline` times the
-reference's expressions (the oracle's torch restatement) on the host cores
-over a bounded sample and scales it to steps/s.
+reference's expressions (the oracle's torch restatement) on the host cores:
+the whole step at C1, a sampled and scaled step otherwise.
 
-  python bench.py [--gpus 1] [--steps 50] [--warmup 3] [--workload c4] [--graph] [--full-logits] [--hf-layers] [--sdpa]
+  python bench.py [--gpus 1] [--steps 50] [--warmup 3] [--workload c4] [--graph] [--full-logits] [--hf-layers]
+                  [--dz-attention]
   python bench.py --kernels [--workload c4]     # per-pass kernel microbench (config C2 style)
 """
 from __future__ import annotations
@@ -75,6 +84,14 @@ def load_traffic(kernel: str, workload: str):
         return None
 
 
+def event_offset(steps: int, warmup: int, interval: int = 50) -> int:
+    """Global step the trainer starts from, so that the DiZO event (after the
+    update of every `interval`-th step, trainer.py:1611) falls on timed step
+    min(steps, interval) - 1 of the window (and every `interval` steps after)."""
+    first = min(steps, interval) - 1
+    return (interval - 1 - (warmup + first)) % interval
+
+
 def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = False, option_head: bool = False,
               enhanced: str = "zo", fused: bool = False, attention: bool = False):
     import numpy as np
@@ -82,7 +99,7 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = Fa
 
     from dizo_amd.synth import SHAPES, Cycle, build_opt, clone_model
     from dizo_amd.timing import KernelTimer
-    from dizo_amd.trainer import ZOArguments, ZOTrainer
+    from dizo_amd.trainer import DIZO_INTERVAL, ZOArguments, ZOTrainer
 
     wl = WORKLOADS[wl_name]
     dtype = _torch_dtype(wl["dtype"])
@@ -94,19 +111,36 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = Fa
     torch.cuda.synchronize()
     log(f"[bench] built {shape.name} {dtype} + anchor in {time.perf_counter() - t0:.1f}s; "
         f"mem {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
-    args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=warmup + steps,
+    offset = event_offset(steps, warmup, DIZO_INTERVAL) if enhanced != "none" else 0
+    args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=offset + warmup + steps,
                        enhanced=None if enhanced == "none" else enhanced, zo_graph=graph, zo_option_head=option_head,
                        zo_fused_mlp=fused, zo_fused_qkv=fused, zo_fused_attention=fused and attention)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches), base_model=base)
+    # start the step counter at `offset` (the LR schedule follows it, trainer.py:1100-1102)
+    tr.state.global_step = offset
+    tr.lr_scheduler.step()
     P = sum(p.numel() for _, p in tr.named_parameters_to_optim)
+    # every DiZO event is timed on its own (device synchronised on both sides)
+    event_s = []
+    dizo_event = tr._dizo_event
+
+    def timed_event(m, seed):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        dizo_event(m, seed)
+        torch.cuda.synchronize()
+        event_s.append(time.perf_counter() - t)
+
+    tr._dizo_event = timed_event
     timer = KernelTimer()
     it = iter(Cycle(batches))
     for i in range(warmup):
         tr.training_step(next(it))
     tr.zo_flush()
     torch.cuda.synchronize()
-    log(f"[bench] warmup {warmup} steps done")
+    log(f"[bench] warmup {warmup} steps done (from global step {offset}; {len(event_s)} DiZO events)")
+    event_s.clear()
     tr.kernel_timer = timer
     if getattr(tr, "dizo_trainer", None) is not None and args.enhanced:
         tr.dizo_trainer.dizo.kernel_timer = timer
@@ -120,47 +154,214 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = Fa
     summary = timer.summary()
     tr.zo_close()
     return dict(elapsed=elapsed, P=P, summary=summary, losses=losses, elem_bytes=torch.finfo(dtype).bits // 8,
-                events=sum(1 for k in range(warmup, warmup + steps) if (k + 1) % 50 == 0) if args.enhanced else 0)
+                events=len(event_s), event_s=list(event_s), offset=offset)
 
 
-def cpu_baseline(wl_name: str, log=print):
-    """The reference's step on the host CPU over one decoder layer, scaled to steps/s.
+def amortised(steps: int, elapsed: float, event_s, interval: int = 50):
+    """(steps/s with one event per `interval` steps, ZO steps/s without events,
+    mean event seconds): steps / (t_steps + t_event * steps / interval)."""
+    t_ev = sum(event_s)
+    t_steps = elapsed - t_ev
+    if not event_s:
+        return steps / elapsed, steps / elapsed, None
+    mean_ev = t_ev / len(event_s)
+    return steps / (t_steps + mean_ev * steps / interval), steps / t_steps, mean_ev
 
-    Sample: one decoder layer of the workload's shape. It times (a) the
-    reference's three perturbations and its update (oracle.ref_torch: the
-    expressions of trainer.py:1438-1442 and 1603-1608 with torch.normal z, in
-    the model dtype) over the layer's 8 attention tensors (q/k/v/out weights
-    and biases, about a third of the layer; scaled to the whole layer by
-    parameter count) and (b) two forwards of one OPT decoder layer on the
-    batch's hidden states (fp32: the host has no fast fp16 GEMM). A full step
-    is estimated as layers x (a + b); the token embedding, LM head, loss and
-    the DiZO event are left out, so the estimate flatters the CPU.
-    """
+
+def _cpu_threads() -> int:
+    """Uses every host core this process may run on; returns the count."""
     import torch
 
-    from dizo_amd.synth import SHAPES, opt_config
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    return cores
+
+
+def _median_s(fn, reps: int = 3, warm: int = 1) -> float:
+    """Median wall time of fn() over `reps` runs after `warm` untimed runs."""
+    import statistics
+
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return float(statistics.median(ts))
+
+
+def _cpu_kv_sample(shape, dtype, gen):
+    """One decoder layer's k_proj and v_proj weights (2 d^2 elements) in the
+    model dtype, and perturbed anchors: the sample the CPU legs time."""
+    import torch
+
+    d = shape.d_model
+    ws = [(torch.randn(d, d, generator=gen) * 0.02).to(dtype) for _ in range(2)]
+    anchors = [(w.float() + 1e-3 * torch.randn(d, d, generator=gen)).to(dtype) for w in ws]
+    return ws, anchors
+
+
+def _cpu_pass_times(params, anchors, reps: int = 3) -> dict:
+    """Median seconds of each pass of the reference over `params` (its
+    expressions with torch.normal z, oracle.ref_torch): perturb +1 / -2 /
+    restore +1 (trainer.py:1438-1442), update (trainer.py:1603-1608), and the
+    projection's norm (trainer.py:455-457), apply (405-436, gamma 0.9 of the
+    norm) and reverse (439-451)."""
+    import torch
+
     from oracle import ref_torch as R
+
+    seed = 123456789
+    ps = [torch.nn.Parameter(p.clone(), requires_grad=False) for p in params]
+    out = {
+        "perturb+1": _median_s(lambda: R.zo_perturb_parameters_sampled(ps, seed, 1, 1e-3), reps),
+        "perturb-2": _median_s(lambda: R.zo_perturb_parameters_sampled(ps, seed, -2, 1e-3), reps),
+        "restore+1": _median_s(lambda: R.zo_perturb_parameters_sampled(ps, seed, 1, 1e-3), reps),
+        "update": _median_s(lambda: R.zo_update_sampled(ps, seed, 0.5, 1e-6), reps),
+        "proj_norm": _median_s(lambda: [torch.norm(p.detach() - a) for p, a in zip(ps, anchors)], reps),
+    }
+    gam = [0.9 * torch.norm(p.detach() - a) for p, a in zip(ps, anchors)]
+    alphas = []
+
+    def apply():
+        alphas[:] = R.apply_constraints(ps, anchors, gam)
+
+    out["proj_apply"] = _median_s(apply, reps)
+    out["proj_reverse"] = _median_s(lambda: R.reverse_constraints(ps, anchors, alphas), reps)
+    return out
+
+
+# algorithmic bytes per element of each pass, in units of the element size
+_PASS_BYTES = {"perturb+1": 2, "perturb-2": 2, "restore+1": 2, "update": 2, "proj_norm": 2, "proj_apply": 3,
+               "proj_reverse": 3}
+
+
+def cpu_baseline_kernels(wl_name: str, log=print) -> dict:
+    """The reference's per-pass expressions on the host cores (the CPU leg of
+    the kernel microbench): median of 3 runs of each pass over one decoder
+    layer's k_proj and v_proj weights of the workload's shape, GB/s from the
+    same algorithmic bytes as the GPU passes."""
+    import torch
+
+    from dizo_amd.synth import SHAPES
 
     wl = WORKLOADS[wl_name]
     shape = SHAPES[wl["shape"]]
     dtype = _torch_dtype(wl["dtype"])
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    d, f = shape.d_model, shape.ffn
-    layer_shapes = [(d, d), (d,)] * 4 + [(d,), (d,), (f, d), (f,), (d, f), (d,), (d,), (d,)]
-    n_layer = sum(int(torch.Size(s).numel()) for s in layer_shapes)
+    cores = _cpu_threads()
+    ws, anchors = _cpu_kv_sample(shape, dtype, torch.Generator().manual_seed(0))
+    n = sum(w.numel() for w in ws)
+    eb = ws[0].element_size()
+    t = _cpu_pass_times(ws, anchors)
+    passes = {k: {"s": v, "GBps": _PASS_BYTES[k] * eb * n / v / 1e9} for k, v in t.items()}
+    for k, v in passes.items():
+        log(f"[cpu] {k:13s} {v['s'] * 1e3:9.1f} ms {v['GBps']:7.2f} GB/s ({n} {wl['dtype']} elements, {cores} threads)")
+    return {
+        "value": passes["perturb+1"]["GBps"],
+        "unit": "GB/s (perturb pass)",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"one {shape.name} decoder layer's k_proj and v_proj weights ({n} {wl['dtype']} elements); "
+                   f"median of 3 runs after 1 warm-up per pass"),
+        "passes": passes,
+    }
+
+
+def cpu_baseline_c1(log=print) -> dict:
+    """Config C1 on the host cores, whole: the reference's MeZO step
+    (oracle.ref_torch.zo_step_sampled: trainer.py:1570-1595 with torch.normal
+    z, full-logit forwards and the option-masked loss of trainer.py:1446-1522)
+    and update (trainer.py:1597-1608) on an OPT-125m fp32 model, batch 16 x 2
+    candidates of length U[32, 64], followed by the DiZO projection with the
+    ratio 0.9 on every k/v tensor (trainer.py:428-436). Median of 3 steps after
+    1 warm-up; per-pass times from the same model."""
+    import copy
+
+    import torch
+    from transformers import OPTForCausalLM
+
+    from dizo_amd.synth import PAD_ID, SHAPES, make_batch, opt_config
+    from oracle import ref_torch as R
+
+    wl = WORKLOADS["c1"]
+    cores = _cpu_threads()
+    torch.manual_seed(0)
+    model = OPTForCausalLM(opt_config(SHAPES[wl["shape"]])).eval()
+    named = [(n, p) for n, p in model.named_parameters() if p.requires_grad]
+    named = [(n, p) for n, p in named if n != "model.decoder.embed_tokens.weight"]  # trainer.py:1160
+    params = [p for _, p in named]
+    kv = [p for n, p in named if n.endswith(("self_attn.k_proj.weight", "self_attn.v_proj.weight"))]
+    anchors = [p.detach().clone() for p in kv]
+    batch = make_batch(wl["batch"], SHAPES[wl["shape"]].vocab, gen=torch.Generator().manual_seed(1),
+                       min_len=wl["min_len"], max_len=wl["max_len"])
+    P = sum(p.numel() for p in params)
+    seeds = iter(range(1000, 2000))
+
+    def step():
+        seed = next(seeds)
+        _, g = R.zo_step_sampled(model, params, batch, seed, 1e-3, PAD_ID)
+        R.zo_update_sampled(params, seed, g, 1e-6)
+        R.apply_ratio(kv, anchors, 0.9)
+
+    with torch.inference_mode():
+        t_step = _median_s(step)
+        t_fwd = _median_s(lambda: R.forward_loss(model, pad_id=PAD_ID, **batch))
+        t_perturb = _median_s(lambda: R.zo_perturb_parameters_sampled(params, 7, 1, 1e-3))
+        t_update = _median_s(lambda: R.zo_update_sampled(params, 7, 0.5, 1e-6))
+        t_apply = _median_s(lambda: R.apply_ratio(kv, anchors, 0.9))
+    Pk = sum(p.numel() for p in kv)
+    log(f"[cpu] c1 step {t_step:.3f}s (forward {t_fwd:.3f}s, perturb {t_perturb:.3f}s, update {t_update:.3f}s, "
+        f"projection {t_apply:.4f}s) on {cores} threads")
+    del model, copy
+    return {
+        "value": 1.0 / t_step,
+        "unit": "steps/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": ("the whole C1 step (MeZO step, update and the 0.9 projection) on an OPT-125m fp32 model, "
+                   "batch 16x2 of length U[32,64]; median of 3 steps after 1 warm-up"),
+        "passes": {
+            "forward": {"s": t_fwd},
+            "perturb": {"s": t_perturb, "GBps": 8 * P / t_perturb / 1e9},
+            "update": {"s": t_update, "GBps": 8 * P / t_update / 1e9},
+            "proj_apply_ratio": {"s": t_apply, "GBps": 12 * Pk / t_apply / 1e9},
+        },
+    }
+
+
+def cpu_baseline_sampled(wl_name: str, log=print) -> dict:
+    """The reference's step on the host cores, estimated from timed samples
+    (the whole C3-C5 step takes minutes on the CPU):
+      * the four ZO passes (trainer.py:1438-1442 x3, 1603-1608; torch.normal
+        z, model dtype) over one decoder layer's k_proj and v_proj weights,
+        scaled to the whole trainable set by parameter count;
+      * two forwards of one OPT decoder layer on the batch's hidden states
+        (fp32: the host has no fast fp16 GEMM), x layers;
+      * the full-logit LM head GEMM of one forward (fp32);
+      * the DiZO event (trainer.py:782-803, every 50 steps): 20 forwards,
+        21 applies and 20 reverses of the projection, amortised per step, the
+        projection passes timed on the same k/v sample and scaled to every
+        layer's k/v.
+    Each factor is reported in the line. The embedding lookup and the loss's
+    log_softmax are left out."""
+    import torch
+
+    from dizo_amd.synth import SHAPES, opt_config
+
+    wl = WORKLOADS[wl_name]
+    shape = SHAPES[wl["shape"]]
+    dtype = _torch_dtype(wl["dtype"])
+    cores = _cpu_threads()
     gen = torch.Generator().manual_seed(0)
-    params = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in layer_shapes[:8]]
-    n_sample = sum(p.numel() for p in params)
-    t0 = time.perf_counter()
-    seed = 123456789
-    R.zo_perturb_parameters_sampled(params, seed, 1, 1e-3)
-    R.zo_perturb_parameters_sampled(params, seed, -2, 1e-3)
-    R.zo_perturb_parameters_sampled(params, seed, 1, 1e-3)
-    R.zo_update_sampled(params, seed, 0.5, 1e-6)
-    t_zo = (time.perf_counter() - t0) * n_layer / n_sample
-    log(f"[cpu] ZO passes over {n_sample} of one layer's {n_layer} params ({dtype}), scaled to the layer: "
-        f"{t_zo:.2f}s on {cores} threads")
+    d, f, Lyr = shape.d_model, shape.ffn, shape.layers
+    n_layer = 4 * d * d + 4 * d + 2 * d + f * d + f + d * f + d + 2 * d  # attention, norms, MLP
+    P = Lyr * n_layer + (shape.max_positions + 2) * d + 2 * d  # + learned positions, final norm
+    ws, anchors = _cpu_kv_sample(shape, dtype, gen)
+    n_kv = sum(w.numel() for w in ws)
+    t = _cpu_pass_times(ws, anchors, reps=1)
+    t_zo = (t["perturb+1"] + t["perturb-2"] + t["restore+1"] + t["update"]) * P / n_kv
+    t_event_proj = Lyr * (21 * t["proj_apply"] + 20 * t["proj_reverse"])
     from transformers.models.opt.modeling_opt import OPTDecoderLayer
 
     cfg = opt_config(shape)
@@ -170,25 +371,41 @@ def cpu_baseline(wl_name: str, log=print):
     seq = wl["fixed_len"] or wl["max_len"]
     hidden = torch.randn(rows, seq, d, generator=gen) * 0.02
     mask = torch.full((seq, seq), float("-inf")).triu(1).reshape(1, 1, seq, seq).expand(rows, 1, seq, seq)
+    head = torch.randn(shape.vocab, d, generator=gen) * 0.02
     with torch.inference_mode():
         layer(hidden[:2], attention_mask=mask[:2])  # warm-up
         t0 = time.perf_counter()
         for _ in range(2):
             layer(hidden, attention_mask=mask)
-        t_fwd = time.perf_counter() - t0
-    log(f"[cpu] two forwards of one decoder layer ({rows}x{seq} tokens, fp32): {t_fwd:.2f}s")
-    step_s = shape.layers * (t_zo + t_fwd)
+        t_fwd2 = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        torch.matmul(hidden.reshape(-1, d), head.t())
+        t_head = time.perf_counter() - t0
+    fwd_per_step = 2 + 20 / 50
+    step_s = t_zo + Lyr * t_fwd2 / 2 * fwd_per_step + t_head * fwd_per_step + t_event_proj / 50
+    log(f"[cpu] {wl_name}: ZO passes {t_zo:.1f}s (sampled {n_kv} of {P} params), layer forwards x2 "
+        f"{t_fwd2:.2f}s, LM head {t_head:.2f}s, event projection {t_event_proj:.1f}s per event; "
+        f"{step_s:.1f}s per step on {cores} threads")
     return {
         "value": 1.0 / step_s,
         "unit": "steps/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"one of {shape.layers} {shape.name} decoder layers: the reference's 3 perturbations + update "
-                   f"(torch.normal z, {wl['dtype']}) timed over the layer's 8 attention tensors ({n_sample} params) "
-                   f"and scaled to its {n_layer} params ({t_zo:.2f}s), and 2 layer forwards on "
-                   f"{rows}x{seq} tokens (fp32; {t_fwd:.2f}s), scaled x{shape.layers}; embedding, LM head, loss "
-                   f"and DiZO event excluded"),
+        "sample": (f"estimated from timed samples: the 4 ZO passes ({wl['dtype']}, torch.normal z) over one "
+                   f"{shape.name} layer's k/v weights ({n_kv} params) scaled to P={P}; 2 forwards of one decoder "
+                   f"layer ({rows}x{seq} tokens, fp32) x {Lyr} layers; the full-logit LM head (fp32); the DiZO "
+                   f"event's 20 forwards and 41 projection passes per 50 steps"),
+        "factors": {"zo_pass_scale": P / n_kv, "layers": Lyr, "forwards_per_step": fwd_per_step,
+                    "event_projection_passes_per_step": 41 / 50, "event_included": True},
+        "components_s": {"zo_passes": t_zo, "layer_forward_x2": t_fwd2, "lm_head": t_head,
+                         "event_projection": t_event_proj, "step": step_s},
     }
+
+
+def cpu_baseline(wl_name: str, log=print) -> dict:
+    """The CPU baseline of a full-step bench line: the whole step at C1, the
+    sampled estimate at C3-C5."""
+    return cpu_baseline_c1(log) if wl_name == "c1" else cpu_baseline_sampled(wl_name, log)
 
 
 def kernel_microbench(wl_name: str, reps: int = 10, log=print):
@@ -338,9 +555,10 @@ def main(argv=None):
     ap.add_argument("--hf-layers", action="store_true",
                     help="run HF's decoder layer code as it is (default: fc1 + ReLU as one GEMM with a ReLU "
                          "epilogue, k/v/q as one GEMM; the same values at the bench shapes)")
-    ap.add_argument("--sdpa", action="store_true",
-                    help="keep SDPA's attention (default with the fused layers: the library's causal attention "
-                         "kernel for unpadded batches)")
+    ap.add_argument("--dz-attention", action="store_true",
+                    help="with the fused layers, run an unpadded batch's causal attention through the library's "
+                         "MFMA kernel (within SDPA's rounding, not bit for bit; default: SDPA)")
+    ap.add_argument("--sdpa", action="store_true", help="SDPA's attention (the default; kept for old command lines)")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the DiZO step path is measured on a "
@@ -361,19 +579,29 @@ def main(argv=None):
     _lib.load()
     if a.kernels:
         res = kernel_microbench(a.workload, log=log)
-        print(json.dumps({"metric": "ZO pass HBM GB/s", "workload": a.workload, **res}), flush=True)
+        line = {"metric": "ZO pass HBM GB/s", "workload": a.workload, **res}
+        if not a.no_cpu_baseline:
+            try:
+                line["cpu_baseline"] = cpu_baseline_kernels(a.workload, log=log)
+            except Exception as e:  # reported, not fatal: the GPU measurement stands
+                line["cpu_baseline"] = {"error": f"{type(e).__name__}: {e}"}
+        print(json.dumps(line), flush=True)
         return 0
+    use_dz_attention = a.dz_attention and not a.hf_layers and not a.sdpa
     r = run_steps(a.workload, a.steps, a.warmup, log=log, graph=a.graph, option_head=not a.full_logits,
-                  enhanced=a.enhanced, fused=not a.hf_layers, attention=not a.sdpa)
+                  enhanced=a.enhanced, fused=not a.hf_layers, attention=use_dz_attention)
     wl = WORKLOADS[a.workload]
-    value = a.steps / r["elapsed"]
+    value, zo_rate, event_s = amortised(a.steps, r["elapsed"], r["event_s"])
     summ = r["summary"]
+    # the dominant library kernel: the fused restore + update + next perturbation
+    # (one launch per steady step, the longest), else the plain perturbation
+    dom_name = "restore_update_perturb" if "restore_update_perturb" in summ else "perturb"
+    dom = summ.get(dom_name)
+    achieved = dom["GBps"] if dom else None
     rmw = [summ[k] for k in ("perturb", "restore_update", "update", "restore_update_perturb") if k in summ]
     rmw_bytes = sum(s["bytes_per_launch"] * s["launches"] for s in rmw)
     rmw_ms = sum(s["total_ms"] for s in rmw)
     rmw_launches = sum(s["launches"] for s in rmw)
-    achieved = rmw_bytes / (rmw_ms * 1e-3) / 1e9 if rmw_ms else None
-    mean_ms = rmw_ms / rmw_launches if rmw_launches else None
     line = {
         "metric": "ZO steps/sec at OPT-13B fp16" if a.workload == "c4" else f"ZO steps/sec ({a.workload})",
         "value": value,
@@ -381,7 +609,7 @@ def main(argv=None):
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": 1000.0 * r["elapsed"] / a.steps,
+        "ms_per_step": 1000.0 / value,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -391,23 +619,34 @@ def main(argv=None):
                                f"candidates, {'seq ' + str(wl['fixed_len']) if wl['fixed_len'] else 'len U[32,64]'}, "
                                f"projection every 50 steps, theta0 resident)",
                    "zo_params": r["P"], "dizo_events_timed": r["events"], "global_batch": 2 * wl["batch"],
+                   "first_global_step": r["offset"],
                    "graph": a.graph, "option_head": not a.full_logits, "fused_gemms": not a.hf_layers,
-                   "attention": "sdpa" if (a.hf_layers or a.sdpa) else "dz_attention_causal (unpadded batches)",
+                   "attention": "dz_attention_causal (unpadded batches)" if use_dz_attention else "sdpa",
                    "enhanced": a.enhanced,
                    "seq_len": wl["fixed_len"] or wl["max_len"],
                    "device": {"name": torch.cuda.get_device_name(0),
                               "compute_units": torch.cuda.get_device_properties(0).multi_processor_count}},
+        "timing": {
+            # value = steps / (t_steps + t_event * steps / 50): one DiZO event per 50 steps
+            "timed_region_s": r["elapsed"],
+            "zo_steps_per_s_without_events": zo_rate,
+            "dizo_event_s": event_s,
+            "dizo_event_s_all": r["event_s"],
+        },
         "roofline": {
-            "kernel": "rmw_kernel (perturb -2 / restore+update / restore+update+next perturb)",
+            "kernel": f"rmw_kernel ({dom_name.replace('_', ' + ')})",
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS if achieved else None,
             "traffic": load_traffic("rmw_kernel", a.workload),
-            "algorithmic_bytes_per_launch": rmw_bytes / rmw_launches if rmw_launches else None,
-            "mean_launch_ms": mean_ms,
-            "launches_per_step": rmw_launches / a.steps,
+            "algorithmic_bytes_per_launch": dom["bytes_per_launch"] if dom else None,
+            "mean_launch_ms": dom["mean_ms"] if dom else None,
+            # all read-modify-write launches of the window together
+            "rmw_all": {"GBps": rmw_bytes / (rmw_ms * 1e-3) / 1e9 if rmw_ms else None,
+                        "frac": rmw_bytes / (rmw_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS if rmw_ms else None,
+                        "launches_per_step": rmw_launches / a.steps},
             # every library pass of the timed region (ZO passes and the DiZO
             # event's projection passes), per ZO parameter and per step
             "bytes_per_param_per_step": sum(v["bytes_per_launch"] * v["launches"] for v in summ.values())

@@ -3,19 +3,24 @@
 // Contents:
 //   * dtype codes used across the C ABI,
 //   * the chunk descriptor that the multi-tensor kernels walk,
-//   * Philox4x32-10, the counter-based generator that regenerates z in registers,
+//   * Philox4x32-7, the counter-based generator that regenerates z in registers,
 //   * the z definition: z(seed, e) for global element index e.
 //
-// Philox4x32-10 follows Salmon, Moraes, Dror and Shaw, "Parallel Random Numbers:
-// As Easy as 1, 2, 3" (SC'11): four 32-bit counter words, a two-word key, ten
+// Philox4x32-R follows Salmon, Moraes, Dror and Shaw, "Parallel Random Numbers:
+// As Easy as 1, 2, 3" (SC'11): four 32-bit counter words, a two-word key, R
 // rounds of two 32x32->64 multiplies by 0xD2511F53 / 0xCD9E8D57, with the key
-// bumped by the Weyl constants 0x9E3779B9 / 0xBB67AE85 between rounds.
+// bumped by the Weyl constants 0x9E3779B9 / 0xBB67AE85 between rounds. z uses
+// R = 7, the fewest rounds the paper found Crush-resistant for Philox4x32 (it
+// passes TestU01's BigCrush; the paper's default of 10 keeps three rounds in
+// hand). Each round costs two 32x32->64 products and two three-way xors per
+// block, and the fused restore + update + next perturbation pass draws two
+// blocks per 8 elements, so the round count sets most of its ALU work.
 //
 // z definition (replaces torch.normal at trainer.py:1441 and :1607):
 //   key  = (seed mod 2^32, seed >> 32)
 //   e    = global element index (tensors laid end to end, each tensor starting
 //          at a multiple of 8, in named_parameters_to_optim order)
-//   w    = Philox4x32-10(counter = (q mod 2^32, q >> 32, stream, 0), key), q = e >> 3
+//   w    = Philox4x32-7(counter = (q mod 2^32, q >> 32, stream, 0), key), q = e >> 3
 //   h    = 16-bit field (e & 7) of w (field j = bits 16*(j&1).. of word j>>1)
 //   z    = (h & 0x8000 ? -1 : +1) * Q_T[h & 0x7fff]
 //   Q_T[i] = RNE_T( Phi^{-1}( 1/2 + (i + 1/2) / 65536 ) )
@@ -76,7 +81,7 @@ DZ_HD void dz_mulhilo32(uint32_t a, uint32_t b, uint32_t* lo, uint32_t* hi) {
   *hi = (uint32_t)(p >> 32);
 }
 
-// Philox4x32 with R rounds (R = 10 is the variant used everywhere here).
+// Philox4x32 with R rounds (z uses R = kDzPhiloxRounds).
 template <int R>
 DZ_HD DzU4 dz_philox4x32(DzU4 c, uint32_t k0, uint32_t k1) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -112,6 +117,10 @@ DZ_HD DzU4 dz_philox4x32(DzU4 c, uint32_t k0, uint32_t k1) {
   return c;
 }
 
+// Rounds of the Philox that defines z (part of the z definition: the oracle's
+// rng.ROUNDS must match).
+constexpr int kDzPhiloxRounds = 7;
+
 // The block of counter q = q_hi * 2^32 + q_lo, with the two words passed
 // apart (a caller whose q_hi is uniform across a wave keeps it scalar).
 DZ_HD DzU4 dz_philox_counter(uint64_t seed, uint32_t stream, uint32_t q_lo, uint32_t q_hi) {
@@ -120,7 +129,7 @@ DZ_HD DzU4 dz_philox_counter(uint64_t seed, uint32_t stream, uint32_t q_lo, uint
   c.y = q_hi;
   c.z = stream;
   c.w = 0u;
-  return dz_philox4x32<10>(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+  return dz_philox4x32<kDzPhiloxRounds>(c, (uint32_t)seed, (uint32_t)(seed >> 32));
 }
 
 DZ_HD DzU4 dz_philox_group(uint64_t seed, uint32_t stream, uint64_t q) {

@@ -51,13 +51,9 @@ struct DzPtrArray {
 #ifndef DZ_RMW_COUNTERS
 #define DZ_RMW_COUNTERS 8
 #endif
-// Workgroups per CU for launches with a 64 KB table (the LDS would allow two),
-// and next-tile prefetch for those launches (measured neutral).
+// Workgroups per CU for launches with a 64 KB table (the LDS would allow two).
 #ifndef DZ_RMW_NARROW_WG_PER_CU
 #define DZ_RMW_NARROW_WG_PER_CU 1
-#endif
-#ifndef DZ_RMW_PREFETCH_NARROW
-#define DZ_RMW_PREFETCH_NARROW 0
 #endif
 constexpr int kRmwThreads = 1024;
 __host__ __device__ constexpr int rmw_groups(int dtype, int mode) {

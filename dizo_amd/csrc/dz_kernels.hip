@@ -136,10 +136,6 @@ struct RmwTraits {
   // Waves per SIMD: 4 with one workgroup per CU (128 VGPRs per lane), 8 when
   // two workgroups share a CU (64 VGPRs).
   static constexpr int kWavesPerEU = (kWide || DZ_RMW_NARROW_WG_PER_CU == 1) ? 4 : 8;
-  // Load tile k+1 while tile k computes: pays off for the two-seed pass, whose
-  // ALU time (two Philox chains per group) is the largest; measured neutral to
-  // negative for the others.
-  static constexpr bool kPrefetch = MODE == kModeRestoreUpdatePerturb || (!kWide && DZ_RMW_PREFETCH_NARROW);
 };
 
 // Table entry for z = +Q_T[i] (qbits = bits of Q_T[i]).
@@ -200,27 +196,92 @@ __device__ __forceinline__ uint32_t add_one(uint32_t a, uint32_t b) {
   }
 }
 
-// Two 16-bit elements (packed in `th`) whose z fields are the halves of `w`
-// (and, for the step-fused mode, whose next-step z fields are the halves of w2).
-// A field's sign bit (bit 15 of its half) negates its table value; once the
-// two lanes' values are packed, that is one xor with w & 0x80008000.
+// The two table entries indexed by the 15-bit fields of a z word (bits 0..14
+// and 16..30; bits 15 and 31 are the signs). The byte offsets index *
+// sizeof(E) take three instructions per word: the sign bits are cleared once,
+// then each half is shifted into place by a word-selecting (SDWA) shift, which
+// reads bits 0..15 or 16..31 of its operand zero-extended (checked on the
+// part against the plain mask-and-shift form). Both offsets are at most
+// 0x7fff * sizeof(E), inside the table.
+template <typename E>
+__device__ __forceinline__ void lookup2(const E* tab, uint32_t w, uint32_t& e0, uint32_t& e1) {
+  const uint32_t m = w & 0x7fff7fffu;
+  uint32_t a0, a1;
+  if constexpr (sizeof(E) == 4) {
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
+        : "=v"(a0)
+        : "v"(m));
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+        : "=v"(a1)
+        : "v"(m));
+  } else {
+    asm("v_lshlrev_b32_sdwa %0, 1, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
+        : "=v"(a0)
+        : "v"(m));
+    asm("v_lshlrev_b32_sdwa %0, 1, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+        : "=v"(a1)
+        : "v"(m));
+  }
+  e0 = (uint32_t)*(const E*)((const char*)tab + a0);
+  e1 = (uint32_t)*(const E*)((const char*)tab + a1);
+}
+
+// Table entries of two 16-bit elements whose z fields are the halves of `w`
+// (and, for the step-fused mode, whose next-step z fields are the halves of
+// w2): the lookups of one packed word.
+struct Entries16 {
+  uint32_t e0, e1, f0, f1;
+};
 template <int DT, int MODE>
-__device__ __forceinline__ uint32_t apply_pair16(uint32_t th, uint32_t w, uint32_t w2,
-                                                 const typename RmwTraits<DT, MODE>::E* tab) {
+__device__ __forceinline__ Entries16 lookup_pair16(uint32_t w, uint32_t w2,
+                                                   const typename RmwTraits<DT, MODE>::E* tab) {
+  Entries16 t;
+  lookup2(tab, w, t.e0, t.e1);
+  if constexpr (MODE == kModeRestoreUpdatePerturb) {
+    lookup2(tab, w2, t.f0, t.f1);
+  } else {
+    t.f0 = t.f1 = 0u;
+  }
+  return t;
+}
+
+// The two elements' new values from their entries. A field's sign bit (bit
+// 15 of its half) negates its table value; once the two lanes' values are
+// packed, that is one xor with w & 0x80008000.
+// R(th + sg * v) lane by lane for sg = +-1.0 (fp16): the product is exact, so
+// the fused multiply-add rounds th +- v once, as the add of the negated value does.
+__device__ __forceinline__ uint32_t fma_sign_pair(uint32_t sg, uint32_t v, uint32_t th) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(dz_half2, sg),
+                                                                __builtin_bit_cast(dz_half2, v),
+                                                                __builtin_bit_cast(dz_half2, th)));
+}
+
+template <int DT, int MODE>
+__device__ __forceinline__ uint32_t combine_pair16(uint32_t th, uint32_t w, uint32_t w2, const Entries16& t) {
+  if constexpr (DT == DZ_F16 && rmw_pair_mode(MODE)) {
+    // entry = b | (-d) << 16 for a positive z; the signs enter as factors
+    // +-1.0 of packed fused multiply-adds (fma_sign_pair), one per add.
+    // +-1.0 in each lane: (w & 0x80008000) | 0x3c003c00 as one three-input
+    // bitwise op (truth table 0xEA: src0 & src1 | src2)
+    const uint32_t sg = __builtin_amdgcn_bitop3_b32(w, 0x80008000u, 0x3c003c00u, 0xEA);
+    uint32_t r = fma_sign_pair(sg, pack_hi(t.e0, t.e1), fma_sign_pair(sg, pack_lo(t.e0, t.e1), th));
+    if constexpr (MODE == kModeRestoreUpdatePerturb) {
+      const uint32_t sg2 = __builtin_amdgcn_bitop3_b32(w2, 0x80008000u, 0x3c003c00u, 0xEA);
+      r = fma_sign_pair(sg2, pack_lo(t.f0, t.f1), r);
+    }
+    return r;
+  }
   const uint32_t sw = w & 0x80008000u;
   if constexpr (!rmw_pair_mode(MODE)) {
-    const uint32_t t0 = tab[w & 0x7fffu], t1 = tab[(w >> 16) & 0x7fffu];
-    return add_pair<DT>(th, (t0 | (t1 << 16)) ^ sw);
+    return add_pair<DT>(th, (t.e0 | (t.e1 << 16)) ^ sw);
   } else {
     // entry = b | (-d) << 16 for a positive z
-    const uint32_t e0 = tab[w & 0x7fffu], e1 = tab[(w >> 16) & 0x7fffu];
-    const uint32_t b = pack_lo(e0, e1) ^ sw;
-    const uint32_t nd = pack_hi(e0, e1) ^ sw;
+    const uint32_t b = pack_lo(t.e0, t.e1) ^ sw;
+    const uint32_t nd = pack_hi(t.e0, t.e1) ^ sw;
     uint32_t r = add_pair<DT>(add_pair<DT>(th, b), nd);
     if constexpr (MODE == kModeRestoreUpdatePerturb) {
       // the next step's +1 perturbation uses the same b (same scale and eps)
-      const uint32_t f0 = tab[w2 & 0x7fffu], f1 = tab[(w2 >> 16) & 0x7fffu];
-      r = add_pair<DT>(r, pack_lo(f0, f1) ^ (w2 & 0x80008000u));
+      r = add_pair<DT>(r, pack_lo(t.f0, t.f1) ^ (w2 & 0x80008000u));
     }
     return r;
   }
@@ -337,63 +398,84 @@ __device__ __forceinline__ void load_tile(const DzChunk& ch, TileRegs<DT, MODE>&
   for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_stream(base + tile_vec_offset<DT>(i));
 }
 
+// Philox block of group u of a full tile: counter zgroup + threadIdx.x +
+// u * kRmwThreads. kUniformHi: the counters' high words agree across the tile
+// (its low word does not wrap), so the high word is wave-uniform and round 0's
+// xor and round 1's first product run on the scalar unit, one v_mad_u64_u32
+// less per block.
+template <bool kUniformHi>
+__device__ __forceinline__ DzU4 tile_block(const DzChunk& ch, uint64_t seed, int u) {
+  if constexpr (kUniformHi) {
+    const uint32_t lo = (uint32_t)ch.zgroup + threadIdx.x + u * kRmwThreads;
+    return dz_philox_counter(seed, kDzStreamParam, lo, (uint32_t)(ch.zgroup >> 32));
+  } else {
+    return dz_philox_group(seed, kDzStreamParam, ch.zgroup + threadIdx.x + u * kRmwThreads);
+  }
+}
+
+// Group u of a full fp32 tile with its z words w (and next-step words w2):
+// the launch's operation applied and the group stored.
+template <int DT, int MODE>
+__device__ __forceinline__ void apply_store_group32(char* base, const TileRegs<DT, MODE>& r, int u, const DzU4& w,
+                                                    const DzU4& w2, const typename RmwTraits<DT, MODE>::E* tab,
+                                                    const DzScalars& sc) {
+  const dz_u32x4 a = r.v[2 * u], b = r.v[2 * u + 1];
+  dz_u32x4 o0, o1;
+  o0.x = apply_one<DT, MODE>(a.x, w.x & 0xffffu, w2.x & 0xffffu, tab, sc);
+  o0.y = apply_one<DT, MODE>(a.y, w.x >> 16, w2.x >> 16, tab, sc);
+  o0.z = apply_one<DT, MODE>(a.z, w.y & 0xffffu, w2.y & 0xffffu, tab, sc);
+  o0.w = apply_one<DT, MODE>(a.w, w.y >> 16, w2.y >> 16, tab, sc);
+  o1.x = apply_one<DT, MODE>(b.x, w.z & 0xffffu, w2.z & 0xffffu, tab, sc);
+  o1.y = apply_one<DT, MODE>(b.y, w.z >> 16, w2.z >> 16, tab, sc);
+  o1.z = apply_one<DT, MODE>(b.z, w.w & 0xffffu, w2.w & 0xffffu, tab, sc);
+  o1.w = apply_one<DT, MODE>(b.w, w.w >> 16, w2.w >> 16, tab, sc);
+  st_stream(base + tile_vec_offset<DT>(2 * u), o0);
+  st_stream(base + tile_vec_offset<DT>(2 * u + 1), o1);
+}
+
+// A full tile as one straight-line block: the Philox blocks of all its
+// groups, then the lookups, adds and stores. Keeping both in one basic block
+// (the branch on the counters' high word is taken once per tile, outside it)
+// lets the scheduler overlap the ALU work of the Philox chains with the LDS
+// lookups; with the chains in a block of their own the two ran one after the
+// other (three-way pass at OPT-13B: 8.9 -> 8.2 ms at equal Philox rounds).
+template <int DT, int MODE, bool kUniformHi>
+__device__ __forceinline__ void tile_body(const DzChunk& ch, const TileRegs<DT, MODE>& r,
+                                          const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc) {
+  constexpr int G = RmwTraits<DT, MODE>::kGroups;
+  constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
+  char* base = (char*)ch.ptr;
+  DzU4 w[G], w2[G];
+#pragma unroll
+  for (int u = 0; u < G; ++u) {
+    w[u] = tile_block<kUniformHi>(ch, sc.seed, u);
+    w2[u] = kTwoSeeds ? tile_block<kUniformHi>(ch, sc.seed2, u) : w[u];
+  }
+#pragma unroll
+  for (int u = 0; u < G; ++u) {
+    if constexpr (DT == DZ_F32) {
+      apply_store_group32<DT, MODE>(base, r, u, w[u], w2[u], tab, sc);
+    } else {
+      dz_u32x4 o;
+      o.x = combine_pair16<DT, MODE>(r.v[u].x, w[u].x, w2[u].x, lookup_pair16<DT, MODE>(w[u].x, w2[u].x, tab));
+      o.y = combine_pair16<DT, MODE>(r.v[u].y, w[u].y, w2[u].y, lookup_pair16<DT, MODE>(w[u].y, w2[u].y, tab));
+      o.z = combine_pair16<DT, MODE>(r.v[u].z, w[u].z, w2[u].z, lookup_pair16<DT, MODE>(w[u].z, w2[u].z, tab));
+      o.w = combine_pair16<DT, MODE>(r.v[u].w, w[u].w, w2[u].w, lookup_pair16<DT, MODE>(w[u].w, w2[u].w, tab));
+      st_stream(base + tile_vec_offset<DT>(u), o);
+    }
+  }
+}
+
 // Applies the launch's operation to a full tile already in registers and stores it.
 template <int DT, int MODE>
 __device__ __forceinline__ void compute_store_tile(const DzChunk& ch, const TileRegs<DT, MODE>& r,
                                                    const typename RmwTraits<DT, MODE>::E* tab,
                                                    const DzScalars& sc) {
   constexpr int G = RmwTraits<DT, MODE>::kGroups;
-  constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
-  char* base = (char*)ch.ptr;
-  // All Philox blocks of the tile first: G (or 2G) independent 10-round
-  // chains the scheduler can interleave.
-  DzU4 w[G], w2[G];
-  // The counters of the tile's groups are zgroup + [0, G * kRmwThreads). When
-  // their high words agree (the low word does not wrap inside the tile), the
-  // high word is wave-uniform: round 0's xor and round 1's first product then
-  // run on the scalar unit, one v_mad_u64_u32 less per block.
-  const uint32_t q_lo = (uint32_t)ch.zgroup, q_hi = (uint32_t)(ch.zgroup >> 32);
-  if (q_lo <= 0xffffffffu - (uint32_t)(G * kRmwThreads - 1)) {
-#pragma unroll
-    for (int u = 0; u < G; ++u) {
-      const uint32_t lo = q_lo + threadIdx.x + u * kRmwThreads;
-      w[u] = dz_philox_counter(sc.seed, kDzStreamParam, lo, q_hi);
-      w2[u] = kTwoSeeds ? dz_philox_counter(sc.seed2, kDzStreamParam, lo, q_hi) : w[u];
-    }
+  if ((uint32_t)ch.zgroup <= 0xffffffffu - (uint32_t)(G * kRmwThreads - 1)) {
+    tile_body<DT, MODE, true>(ch, r, tab, sc);
   } else {
-#pragma unroll
-    for (int u = 0; u < G; ++u) {
-      const uint64_t q = ch.zgroup + threadIdx.x + u * kRmwThreads;
-      w[u] = dz_philox_group(sc.seed, kDzStreamParam, q);
-      w2[u] = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, q) : w[u];
-    }
-  }
-  if constexpr (DT != DZ_F32) {
-#pragma unroll
-    for (int u = 0; u < G; ++u) {
-      dz_u32x4 o;
-      o.x = apply_pair16<DT, MODE>(r.v[u].x, w[u].x, w2[u].x, tab);
-      o.y = apply_pair16<DT, MODE>(r.v[u].y, w[u].y, w2[u].y, tab);
-      o.z = apply_pair16<DT, MODE>(r.v[u].z, w[u].z, w2[u].z, tab);
-      o.w = apply_pair16<DT, MODE>(r.v[u].w, w[u].w, w2[u].w, tab);
-      st_stream(base + tile_vec_offset<DT>(u), o);
-    }
-  } else {
-#pragma unroll
-    for (int u = 0; u < G; ++u) {
-      const dz_u32x4 a = r.v[2 * u], b = r.v[2 * u + 1];
-      dz_u32x4 o0, o1;
-      o0.x = apply_one<DT, MODE>(a.x, w[u].x & 0xffffu, w2[u].x & 0xffffu, tab, sc);
-      o0.y = apply_one<DT, MODE>(a.y, w[u].x >> 16, w2[u].x >> 16, tab, sc);
-      o0.z = apply_one<DT, MODE>(a.z, w[u].y & 0xffffu, w2[u].y & 0xffffu, tab, sc);
-      o0.w = apply_one<DT, MODE>(a.w, w[u].y >> 16, w2[u].y >> 16, tab, sc);
-      o1.x = apply_one<DT, MODE>(b.x, w[u].z & 0xffffu, w2[u].z & 0xffffu, tab, sc);
-      o1.y = apply_one<DT, MODE>(b.y, w[u].z >> 16, w2[u].z >> 16, tab, sc);
-      o1.z = apply_one<DT, MODE>(b.z, w[u].w & 0xffffu, w2[u].w & 0xffffu, tab, sc);
-      o1.w = apply_one<DT, MODE>(b.w, w[u].w >> 16, w2[u].w >> 16, tab, sc);
-      st_stream(base + tile_vec_offset<DT>(2 * u), o0);
-      st_stream(base + tile_vec_offset<DT>(2 * u + 1), o1);
-    }
+    tile_body<DT, MODE, false>(ch, r, tab, sc);
   }
 }
 
@@ -456,8 +538,9 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
   const uint64_t nch = nchunks;
   // Pipeline kept by wave 0: while tile k streams, the index of tile k+3 is
   // taken from the counter and the descriptor of tile k+2 is loaded, so
-  // neither latency sits between two tiles. The two-seed pass (Tr::kPrefetch)
-  // also loads tile k+1's data before computing tile k.
+  // neither latency sits between two tiles. A tile's data is loaded when its
+  // turn comes: loading tile k + 1 during tile k measured slower for every
+  // mode once the three-way pass's ALU work had shrunk.
   if (threadIdx.x == 0) {
     uint64_t c[3];
     for (int i = 0; i < 3; ++i) {
@@ -468,17 +551,7 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
     if (c[1] < nch) sdesc[1] = chunks[c[1]];
   }
   __syncthreads();
-  TileRegs<DT, MODE> cur, nxt;
-  bool have_cur = false;
-  if constexpr (Tr::kPrefetch) {
-    if (sidx[0] < nchunks) {
-      const DzChunk c0 = uniform_chunk(sdesc[0]);
-      if (full_tile<DT, MODE>(c0)) {
-        load_tile<DT, MODE>(c0, cur);
-        have_cur = true;
-      }
-    }
-  }
+  TileRegs<DT, MODE> cur;
   for (uint32_t k = 0;; ++k) {
     const uint32_t c = sidx[k % 4];
     if (c >= nchunks) break;
@@ -502,18 +575,8 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
         have_desc = true;
       }
     }
-    bool have_next = false;
-    if constexpr (Tr::kPrefetch) {
-      if (sidx[(k + 1) % 4] < nchunks) {
-        const DzChunk cn = uniform_chunk(sdesc[(k + 1) % 3]);
-        if (full_tile<DT, MODE>(cn)) {
-          load_tile<DT, MODE>(cn, nxt);
-          have_next = true;
-        }
-      }
-    }
     if (full_tile<DT, MODE>(ch)) {
-      if (!have_cur) load_tile<DT, MODE>(ch, cur);
+      load_tile<DT, MODE>(ch, cur);
       compute_store_tile<DT, MODE>(ch, cur, tab, sc);
     } else {
       rmw_partial<DT, MODE>(ch, tab, sc);
@@ -530,10 +593,6 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
       }
     }
     __syncthreads();
-    if constexpr (Tr::kPrefetch) {
-      cur = nxt;
-      have_cur = have_next;
-    }
   }
   if (threadIdx.x == 0) {
     const uint32_t done = atomicAdd(counters + kCounters * kCounterStride, 1u);

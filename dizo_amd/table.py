@@ -227,7 +227,7 @@ def normals(seed: int, stream_id: int, offset: int, n: int, dtype: torch.dtype,
 
 def philox_blocks(seed: int, stream_id: int, q0: int, n: int, device: torch.device, *,
                   stream=None) -> torch.Tensor:
-    """n Philox4x32-10 blocks as an (n, 4) int32 tensor (bit patterns of uint32)."""
+    """n blocks of the z generator (Philox4x32-7) as an (n, 4) int32 tensor (bit patterns of uint32)."""
     out = torch.empty((n, 4), dtype=torch.int32, device=device)
     with torch.cuda.device(device):
         L.call("dz_philox", int(seed), int(stream_id), int(q0), int(n), out.data_ptr(),
@@ -244,7 +244,7 @@ def normal_table(dtype: torch.dtype) -> torch.Tensor:
 
 
 def philox_host(seed: int, stream_id: int, q: int) -> list[int]:
-    """One Philox4x32-10 block computed by the library on the host."""
+    """One block of the z generator (Philox4x32-7) computed by the library on the host."""
     out = (C.c_uint32 * 4)()
     L.call("dz_philox_host", int(seed), int(stream_id), int(q), out)
     return list(out)

@@ -33,7 +33,7 @@ What differs from the reference, by design:
     reference's (code that reads parameter storage directly between two steps
     calls ``zo_flush()`` first);
   * ``torch.normal`` z (torch's Philox + Box-Muller) is replaced by the
-    library's z: Philox4x32-10 keyed by the seed, 16 bits per element mapped
+    library's z: Philox4x32-7 keyed by the seed, 16 bits per element mapped
     through a 15-bit normal quantile table. Seeds, scaling factors, rounding
     and the update formula are the reference's.
 """

@@ -56,7 +56,7 @@ const char* dz_last_error(void);
  * Replaces the normal transform inside torch.normal, trainer.py:1441,1607. */
 int32_t dz_normal_table(int32_t dtype, void* out, int64_t n_entries);
 
-/* Philox4x32-10 block for key = seed, counter = (q, stream, 0), on the host. */
+/* Block of the z generator, Philox4x32-7, for key = seed, counter = (q, stream, 0), on the host. */
 int32_t dz_philox_host(uint64_t seed, uint32_t stream_id, uint64_t q, uint32_t out[4]);
 
 /* ---- parameter tables --------------------------------------------------- */
@@ -125,7 +125,7 @@ int32_t dz_normals(uint64_t seed, uint32_t stream_id, uint64_t offset, int64_t n
 /* The z that dz_perturb/dz_update apply to tensor idx of a ZO table. */
 int32_t dz_export_z(const dz_table* t, uint64_t seed, int32_t idx, void* d_out, void* stream);
 
-/* n Philox blocks (4 x uint32 each) for counters q0 .. q0+n-1. */
+/* n blocks of the z generator, Philox4x32-7 (4 x uint32 each), for counters q0 .. q0+n-1. */
 int32_t dz_philox(uint64_t seed, uint32_t stream_id, uint64_t q0, int64_t n, uint32_t* d_out,
                   void* stream);
 

@@ -9,7 +9,7 @@ Modules
   arith     numpy restatement of the reference's per-element arithmetic
             (trainer.py:1442, 1608, 1587, 428-464, 545-614, 1100-1102) with the
             PyTorch rounding recipe: one fp32 op, then RNE to the dtype.
-  rng       Philox4x32-10 (Salmon et al., SC'11) and the z definition
+  rng       Philox4x32-R (Salmon et al., SC'11; z uses R = 7) and the z definition
             z(seed, stream, e) = sign * Q_T[15-bit index], with Q_T built from
             scipy.special.ndtri and exact rational rounding.
   ref_torch the reference's own expressions (trainer.py:1429-1444, 1597-1608,

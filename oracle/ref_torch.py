@@ -165,3 +165,58 @@ def dizo_zo_iteration(news, anchors, gammas: list, init: bool, z_gamma: Sequence
             gammas[i] = torch.clip(gammas[i] - step_size * ts[i] * grad * zs[i], (1 - tau) * ts[i],
                                    (1 + tau) * ts[i])
     return ts, loss1, loss2
+
+
+def forward_loss(model, input_ids, attention_mask, labels, option_len, num_options, pad_id: int) -> torch.Tensor:
+    """trainer.py:1446-1522 (classification branch) with torch ops: the full
+    logits, the per-row option masking loop and the option-position
+    log-probability mean, then the cross-entropy over each example's
+    candidates. The CPU baseline's forward and loss."""
+    import torch.nn.functional as F
+
+    with torch.no_grad():
+        logits = model(input_ids=input_ids, attention_mask=attention_mask).logits
+    shift_logits = logits[..., :-1, :].contiguous()
+    shift_labels = torch.clone(input_ids)[..., 1:].contiguous()
+    shift_labels[shift_labels == pad_id] = -100
+    for i, n in enumerate(option_len.tolist()):
+        shift_labels[i, :-n] = -100
+    loss_fct = torch.nn.CrossEntropyLoss(ignore_index=-100)
+    log_probs = F.log_softmax(shift_logits, dim=-1)
+    mask = shift_labels != -100
+    shift_labels[~mask] = 0
+    selected = torch.gather(log_probs, dim=-1, index=shift_labels.unsqueeze(-1)).squeeze(-1)
+    selected = (selected * mask).sum(-1) / mask.sum(-1)
+    nopt = num_options.tolist()
+    if any(x != nopt[0] for x in nopt):
+        loss, start, count = 0, 0, 0
+        while start < len(nopt):
+            end = start + nopt[start]
+            loss = loss_fct(selected[start:end].unsqueeze(0), labels[start:end][0].unsqueeze(0)) + loss
+            count += 1
+            start = end
+        return loss / count
+    return loss_fct(selected.view(-1, nopt[0]), labels.view(-1, nopt[0])[:, 0])
+
+
+def zo_step_sampled(model, params: Sequence[torch.Tensor], batch: dict, seed: int, zo_eps: float,
+                    pad_id: int):
+    """trainer.py:1570-1595 verbatim (torch.normal z): +1, loss1, -2, loss2,
+    projected_grad, +1. Returns (loss1, projected_grad)."""
+    zo_perturb_parameters_sampled(params, seed, 1, zo_eps)
+    loss1 = forward_loss(model, pad_id=pad_id, **batch)
+    zo_perturb_parameters_sampled(params, seed, -2, zo_eps)
+    loss2 = forward_loss(model, pad_id=pad_id, **batch)
+    g = projected_grad(loss1, loss2, zo_eps)
+    zo_perturb_parameters_sampled(params, seed, 1, zo_eps)
+    return loss1, g
+
+
+def apply_ratio(news: Sequence[torch.Tensor], anchors: Sequence[torch.Tensor], alpha: float) -> None:
+    """trainer.py:428-436 with the ratio supplied (alpha in place of
+    constraint / (norm + 1e-8)): new <- (new - anchor) * alpha + anchor."""
+    for new_para, anchor_para in zip(news, anchors):
+        v = (new_para.detach() - anchor_para.detach()) * alpha
+        temp = v + anchor_para.detach()
+        with torch.no_grad():
+            new_para.copy_(temp)

@@ -1,14 +1,16 @@
-"""Philox4x32-10 and the z definition, restated in numpy (test oracle only).
+"""Philox4x32-R and the z definition, restated in numpy (test oracle only).
 
-Philox4x32-10 follows Salmon, Moraes, Dror and Shaw, "Parallel Random
+Philox4x32-R follows Salmon, Moraes, Dror and Shaw, "Parallel Random
 Numbers: As Easy as 1, 2, 3" (SC'11). One round maps counter (c0, c1, c2, c3)
 under key (k0, k1) to
   (mulhi(M1, c2) ^ c1 ^ k0, mullo(M1, c2), mulhi(M0, c0) ^ c3 ^ k1, mullo(M0, c0))
 with M0 = 0xD2511F53, M1 = 0xCD9E8D57; the key is bumped by the Weyl
-constants 0x9E3779B9, 0xBB67AE85 between rounds.
+constants 0x9E3779B9, 0xBB67AE85 between rounds. The paper's default is
+R = 10; z uses R = ROUNDS = 7, the fewest rounds the paper found
+Crush-resistant for Philox4x32 (the library's dz_common.h defines the same).
 
 The z that replaces torch.normal (trainer.py:1441, 1607) is defined as
-  q = e >> 3, j = e & 7, w = Philox(counter = (q lo, q hi, stream, 0), key = seed)
+  q = e >> 3, j = e & 7, w = Philox4x32-7(counter = (q lo, q hi, stream, 0), key = seed)
   h = 16-bit field j of w (word j >> 1, half j & 1)
   z = (-1)^(h >> 15) * Q_T[h & 0x7fff],  Q_T[i] = RNE_T(Phi^-1(1/2 + (i + 1/2) / 65536)).
 """
@@ -22,6 +24,7 @@ import numpy as np
 
 from .arith import BF16, F16, F32
 
+ROUNDS = 7  # rounds of the Philox that defines z
 M0, M1 = 0xD2511F53, 0xCD9E8D57
 W0, W1 = 0x9E3779B9, 0xBB67AE85
 MASK32 = 0xFFFFFFFF
@@ -62,11 +65,12 @@ def philox_scalar(ctr, key, rounds: int = 10):
     return c
 
 
-def philox_groups(seed: int, stream: int, q) -> np.ndarray:
-    """Blocks for counters q (uint64 array) under key = seed: (n, 4) uint32."""
+def philox_groups(seed: int, stream: int, q, rounds: int = ROUNDS) -> np.ndarray:
+    """Blocks for counters q (uint64 array) under key = seed: (n, 4) uint32
+    (the z generator's Philox4x32-7 unless `rounds` says otherwise)."""
     q = np.asarray(q, dtype=np.uint64)
     return philox4x32(q & np.uint64(MASK32), q >> np.uint64(32), np.uint64(stream), np.uint64(0),
-                      seed & MASK32, (seed >> 32) & MASK32)
+                      seed & MASK32, (seed >> 32) & MASK32, rounds)
 
 
 # --------------------------------------------------------- quantile table ---

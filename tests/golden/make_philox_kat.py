@@ -1,14 +1,15 @@
-"""Writes tests/golden/philox_kat.json: Philox4x32-10 known answers.
+"""Writes tests/golden/philox_kat.json: Philox4x32-10 and Philox4x32-7 known answers.
 
 Two independent sources:
   * the Random123 known-answer vectors for philox4x32-10 (Salmon et al.,
     SC'11 distribution, kat_vectors), typed in below;
   * PyTorch's header-only engine ``at::Philox4_32`` (ATen/core/PhiloxRNGEngine.h,
     BSD source shipped with the installed torch), compiled with g++ and run
-    for a set of (seed, subsequence, offset) triples. That engine keys
-    Philox with the seed and uses counter = (offset, subsequence), so its
-    first output block equals our block for key = seed,
-    counter = (q = offset, stream = subsequence).
+    for a set of (seed, subsequence, offset) triples, with its default 10
+    rounds and with 7 (the engine takes the round count as an argument; 7 is
+    the z generator's). That engine keys Philox with the seed and uses
+    counter = (offset, subsequence), so its first output block equals our
+    block for key = seed, counter = (q = offset, stream = subsequence).
 
 Run: python tests/golden/make_philox_kat.py
 """
@@ -41,11 +42,12 @@ PROG = r"""
 #include <cstdio>
 #include <cstdlib>
 int main(int argc, char** argv) {
-  for (int i = 1; i + 2 < argc; i += 3) {
+  int rounds = atoi(argv[1]);
+  for (int i = 2; i + 2 < argc; i += 3) {
     unsigned long long seed = strtoull(argv[i], 0, 10), sub = strtoull(argv[i+1], 0, 10),
                        off = strtoull(argv[i+2], 0, 10);
     at::Philox4_32 eng(seed, sub, off);
-    unsigned a = eng(), b = eng(), c = eng(), d = eng();
+    unsigned a = eng(rounds), b = eng(rounds), c = eng(rounds), d = eng(rounds);
     printf("%u %u %u %u\n", a, b, c, d);
   }
   return 0;
@@ -53,7 +55,7 @@ int main(int argc, char** argv) {
 """
 
 
-def torch_engine_blocks(cases):
+def torch_engine_blocks(cases, rounds: int = 10):
     inc = os.path.join(os.path.dirname(torch.__file__), "include")
     with tempfile.TemporaryDirectory() as td:
         src = os.path.join(td, "kat.cpp")
@@ -62,21 +64,24 @@ def torch_engine_blocks(cases):
             f.write(PROG)
         subprocess.run(["g++", "-O1", "-std=c++17", f"-I{inc}", src, "-o", exe], check=True)
         args = [str(x) for c in cases for x in c]
-        out = subprocess.run([exe, *args], check=True, capture_output=True, text=True).stdout
+        out = subprocess.run([exe, str(rounds), *args], check=True, capture_output=True, text=True).stdout
     return [[int(x) for x in line.split()] for line in out.strip().splitlines()]
 
 
 def main():
     blocks = torch_engine_blocks(CASES)
+    blocks7 = torch_engine_blocks(CASES, rounds=7)
     data = {
         "random123": RANDOM123_KAT,
         "torch_engine": [{"seed": s, "stream": sub, "q": off, "block": b}
                          for (s, sub, off), b in zip(CASES, blocks)],
+        "torch_engine_r7": [{"seed": s, "stream": sub, "q": off, "block": b}
+                            for (s, sub, off), b in zip(CASES, blocks7)],
         "source": "tests/golden/make_philox_kat.py",
     }
     with open(os.path.join(HERE, "philox_kat.json"), "w") as f:
         json.dump(data, f, indent=1)
-    print(f"wrote {len(blocks)} torch-engine blocks")
+    print(f"wrote {len(blocks)} + {len(blocks7)} torch-engine blocks (10 and 7 rounds)")
 
 
 if __name__ == "__main__":

@@ -38,6 +38,7 @@ def test_flags_and_workloads():
     assert set(bench.WORKLOADS) == {"c1", "c3", "c4", "c5"}
     c4 = bench.WORKLOADS["c4"]
     assert (c4["shape"], c4["dtype"], c4["batch"], c4["fixed_len"]) == ("opt-13b", "float16", 16, 128)
-    for flags in (["--graph"], ["--full-logits"], ["--hf-layers"], ["--sdpa"], ["--kernels"], ["--enhanced", "fo"],
+    for flags in (["--graph"], ["--full-logits"], ["--hf-layers"], ["--sdpa"], ["--dz-attention"], ["--kernels"],
+                  ["--enhanced", "fo"],
                   ["--workload", "c5"], ["--no-cpu-baseline"]):
         assert bench.main(flags + ["--gpus", "3"]) == 2  # parses, then stops at the one-GPU check

@@ -1,6 +1,7 @@
 """A non-Python host of the C ABI: a C99 program compiled with gcc against
 include/dizo_amd.h and linked with libdizo_amd.so calls the host-side entry
-points (no GPU): the version, a Philox4x32-10 block and the quantile table.
+points (no GPU): the version, a block of the z generator (Philox4x32-7) and the
+quantile table.
 Its output matches the oracle."""
 import os
 import shutil

@@ -18,8 +18,9 @@ and learning-rate schedule:
   * config C2 (kernel passes over the OPT-2.7B trainable set): separate
     passes (+1, -2, +1, update) and fused passes give the same weights bit for
     bit, and match the reference's expressions on sampled tensors;
-  * config C5's scale (OPT-30B bf16): the fused passes and the projection on
-    sampled tensors and groups against the reference's expressions.
+  * config C5's scale (OPT-30B bf16) and config C4, the headline (OPT-13B
+    fp16): the fused passes and the projection on sampled tensors and groups
+    against the reference's expressions.
 """
 import copy
 import sys
@@ -353,6 +354,82 @@ def test_c5_opt30b_bf16_passes_and_projection():
         r = (keep[i] - t0[i]) * a + t0[i]
         r = (r - t0[i]) / a + t0[i]
         assert _same(th[i], r), names[i]
+    want = torch.stack([_lib_norm(th[i] - t0[i]) for i in gs])
+    assert _same(norms[gs], want)
+    ptab.close()
+
+
+def test_c4_opt13b_fp16_passes_and_projection():
+    """Config C4, the headline workload (OPT-13B fp16: 643 trainable tensors,
+    12,596,080,640 elements; 80 projected k/v groups): +1, -2 and the fused
+    restore+update+next perturb over the whole set, then sampled tensors
+    (embed_positions, the first k_proj weight, a bias, the middle tensor, the
+    last) against the reference's expressions (trainer.py:1438-1442,
+    1603-1608) fed the exported z; then one DiZO event's passes over all 80
+    groups (trainer.py:405-451): the norms, an apply with alpha = gamma /
+    (norm + 1e-8) for gamma = 0.9 of the norm, and the reverse with the norms
+    of the reversed theta, on sampled groups against the reference's torch
+    expressions with the library's norm definition."""
+    from dizo_amd import _lib as L
+    from dizo_amd.dizo import DiZO
+    from dizo_amd.synth import build_opt
+    from dizo_amd.table import ProjTable
+    from dizo_amd.trainer import _ZOTables, select_trainable
+    dt, eps, lr = torch.float16, 1e-3, 9.5e-7
+    g = float(torch.tensor(-3.4375, dtype=dt))
+    model = build_opt("opt-13b", dt, "cuda", seed=0)
+    named, exclude = select_trainable(model)
+    assert len(named) == 643 and sum(p.numel() for _, p in named) == 12_596_080_640
+    names = [n for n, _ in named]
+    bias = names.index("model.decoder.layers.3.self_attn.q_proj.bias")
+    sample = [0, 1, bias, len(named) // 2, len(named) - 1]
+    assert names[0] == "model.decoder.embed_positions.weight"
+    before = {i: named[i][1].detach().clone() for i in sample}
+    tabs = _ZOTables(named)
+    (tab, _), = tabs.tables
+    s1, s2 = 31337, 4242
+    tab.perturb(s1, 1.0, eps)
+    tab.perturb(s1, -2.0, eps)
+    tab.restore_update_perturb(s1, s2, eps, g, lr)
+    torch.cuda.synchronize()
+    for i in sample:
+        z1, z2 = tab.export_z(s1, i), tab.export_z(s2, i)
+        ref = [before[i].clone()]
+        R.zo_perturb_parameters_recipe(ref, [z1], 1, eps)
+        R.zo_perturb_parameters_recipe(ref, [z1], -2, eps)
+        R.zo_perturb_parameters_recipe(ref, [z1], 1, eps)
+        R.zo_update_recipe(ref, [z1], g, lr)
+        R.zo_perturb_parameters_recipe(ref, [z2], 1, eps)
+        assert _same(ref[0], named[i][1].data), names[i]
+    del before
+    tabs.close()
+    cname = DiZO(model, "l2norm", exclude).constraints_name
+    assert len(cname) == 80
+    params = dict(model.named_parameters())
+    th = [params[n].data for n in cname]
+    t0 = [(t.float() + 2e-3).to(dt) for t in th]
+    ptab = ProjTable(th, t0)
+    norms = torch.empty(80, dtype=dt, device="cuda")
+    ptab.group_sumsq(norm_T=norms)
+    gs = [0, 1, 39, 79]
+    want = torch.stack([_lib_norm(th[i] - t0[i]) for i in gs])
+    assert _same(norms[gs], want)
+    gamma = (norms.float() * 0.9).to(dt)
+    alpha = (gamma / (norms + 1e-8)).contiguous()  # trainer.py:464, in the model dtype
+    keep = {i: th[i].clone() for i in gs}
+    ptab.project(alpha, L.DZ_PROJ_APPLY)
+    torch.cuda.synchronize()
+    for i in gs:
+        r = [keep[i].clone()]
+        R.apply_constraints(r, [t0[i]], [gamma[i:i + 1]], norm=_lib_norm)
+        assert _same(th[i], r[0]), cname[i]
+        keep[i] = r[0]
+    ptab.project(alpha, L.DZ_PROJ_REVERSE_SUMSQ, norm_T=norms)
+    torch.cuda.synchronize()
+    for i in gs:
+        r = [keep[i]]
+        R.reverse_constraints(r, [t0[i]], [alpha[i:i + 1]])
+        assert _same(th[i], r[0]), cname[i]
     want = torch.stack([_lib_norm(th[i] - t0[i]) for i in gs])
     assert _same(norms[gs], want)
     ptab.close()

@@ -236,3 +236,44 @@ def test_llama_without_pad_id_matches_bruteforce():
                                   b["option_len"].tolist(), b["num_options"].tolist(), None)
     assert float(full) == pytest.approx(want, rel=1e-5, abs=1e-6)
     assert float(head) == pytest.approx(want, rel=1e-5, abs=1e-6)
+
+
+@pytest.mark.parametrize("seed", [0, 3])
+def test_reference_forward_loss_restatement_matches_bruteforce(tiny_model, seed):
+    """oracle.ref_torch.forward_loss (the CPU baseline's forward: full logits and
+    the reference's own per-row masking loop, trainer.py:1446-1522) against the
+    float64 brute force."""
+    from dizo_amd.synth import PAD_ID, make_batch
+    from oracle import ref_torch as R
+
+    b = make_batch(3, 512, gen=torch.Generator().manual_seed(seed), min_len=5, max_len=12)
+    if seed == 3:
+        b["input_ids"][1, -4] = PAD_ID
+    with torch.no_grad():
+        got = R.forward_loss(tiny_model, pad_id=PAD_ID, **b)
+        logits = tiny_model(input_ids=b["input_ids"], attention_mask=b["attention_mask"]).logits
+    want = OL.classification_loss(logits.double().numpy(), b["input_ids"].numpy(), b["labels"].tolist(),
+                                  b["option_len"].tolist(), b["num_options"].tolist(), PAD_ID)
+    assert float(got) == pytest.approx(want, rel=1e-5, abs=1e-6)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_reference_apply_ratio_matches_arith(dt):
+    """oracle.ref_torch.apply_ratio (trainer.py:428-436 with the ratio supplied)
+    against oracle.arith.apply with alpha rounded to the dtype, and alpha = 1
+    leaving R(R(theta - theta0) + theta0)."""
+    from oracle import arith as A
+    from oracle import ref_torch as R
+
+    name = {torch.float16: A.F16, torch.bfloat16: A.BF16, torch.float32: A.F32}[dt]
+    view = torch.int32 if dt == torch.float32 else torch.int16
+    gen = torch.Generator().manual_seed(2)
+    th = (torch.randn(4099, generator=gen) * 0.02).to(dt)
+    t0 = (th.float() + 1e-3 * torch.randn(4099, generator=gen)).to(dt)
+    for a in (0.9, 1.0):
+        p = [th.clone()]
+        R.apply_ratio(p, [t0], torch.tensor(a, dtype=dt))
+        bits = lambda x: x.view(view).numpy().view(np.uint32 if dt == torch.float32 else np.uint16)  # noqa: E731
+        alpha_bits = bits(torch.tensor([a], dtype=dt))
+        want = A.apply(bits(th), bits(t0), np.repeat(alpha_bits, th.numel()), name)
+        np.testing.assert_array_equal(bits(p[0]), want)

@@ -29,18 +29,48 @@ def test_random123_kat_vectors(kat):
 
 def test_torch_engine_kat(kat):
     for e in kat["torch_engine"]:
+        got = rng.philox_groups(e["seed"], e["stream"], np.array([e["q"]], dtype=np.uint64), rounds=10)[0]
+        assert got.tolist() == e["block"], e
+
+
+def test_torch_engine_kat_seven_rounds(kat):
+    # the z generator (Philox4x32-7) against torch's engine run with 7 rounds
+    assert rng.ROUNDS == 7
+    for e in kat["torch_engine_r7"]:
         got = rng.philox_groups(e["seed"], e["stream"], np.array([e["q"]], dtype=np.uint64))[0]
         assert got.tolist() == e["block"], e
 
 
-def test_fewer_rounds_differ():
+def _more_rounds(block, key, done: int, extra: int):
+    """`extra` further Philox rounds applied to the output of `done` rounds
+    (the key bumped `done` times first)."""
+    k0 = (key[0] + done * rng.W0) & rng.MASK32
+    k1 = (key[1] + done * rng.W1) & rng.MASK32
+    return rng.philox_scalar(block, [k0, k1], rounds=extra) if extra else list(block)
+
+
+def test_seven_rounds_are_a_prefix_of_ten(kat):
+    # Rounds 8-10 applied to the 7-round output reproduce the Random123 10-round
+    # vectors. A round is a bijection of the counter for a fixed key, so a wrong
+    # 7-round block cannot continue into the right 10-round one.
+    for ctr, key, expected in kat["random123"]:
+        b7 = rng.philox_scalar(ctr, key, rounds=7)
+        assert _more_rounds(b7, key, 7, 3) == expected
+        assert b7 != expected
+
+
+def test_fewer_rounds_differ(kat):
     # A dropped round must not pass the KAT (guards the round count).
     assert rng.philox_scalar([0, 0, 0, 0], [0, 0], rounds=9) != [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]
+    e = kat["torch_engine_r7"][0]
+    for r in (6, 8):
+        got = rng.philox_groups(e["seed"], e["stream"], np.array([e["q"]], dtype=np.uint64), rounds=r)[0]
+        assert got.tolist() != e["block"]
 
 
 def test_library_host_philox_matches_oracle(kat):
     from dizo_amd import table as T
-    for e in kat["torch_engine"]:
+    for e in kat["torch_engine_r7"]:
         assert T.philox_host(e["seed"], e["stream"], e["q"]) == e["block"]
     r = np.random.default_rng(0)
     for _ in range(200):
