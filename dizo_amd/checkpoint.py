@@ -47,7 +47,9 @@ from . import _lib as L
 from ._lib import DzError
 
 FORMAT = "dizo-amd-zo-journal"
-VERSION = 1
+# 2: z drawn from Philox4x32-7 (version 1 journals and checkpoints were made
+# with Philox4x32-10 and do not replay on this library)
+VERSION = 2
 STATE_FORMAT = "dizo-amd-zo-checkpoint"
 PROJ_MODES = {"apply": L.DZ_PROJ_APPLY, "apply_f32": L.DZ_PROJ_APPLY_F32ALPHA, "reverse": L.DZ_PROJ_REVERSE}
 _DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
