@@ -185,6 +185,27 @@ int32_t check_range(uint64_t p, uint64_t bytes, const char* what, int32_t i) {
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point (dz_group_sumsq_static): device
+// memory the library never allocates at run time. Layout: the projection
+// kernel's work counters, the group -> first chunk index, the chunk
+// descriptors and the per-chunk partial sums, for at most kStaticMaxGroups
+// groups and kStaticMaxChunks chunks of kProjChunk elements (8.6 G elements).
+// Each device holds its own copy, at its own address (see static_scratch).
+// ---------------------------------------------------------------------------
+namespace {
+constexpr uint32_t kStaticMaxGroups = 4096;
+constexpr uint32_t kStaticMaxChunks = 1u << 18;
+constexpr size_t kStaticOffCounters = 0;
+constexpr size_t kStaticOffGroupBegin = 4096;
+constexpr size_t kStaticOffChunks = kStaticOffGroupBegin + ((kStaticMaxGroups + 1) * 4 + 255) / 256 * 256;
+constexpr size_t kStaticOffPartials = kStaticOffChunks + (size_t)kStaticMaxChunks * sizeof(DzChunk);
+constexpr size_t kStaticBytes = kStaticOffPartials + (size_t)kStaticMaxChunks * sizeof(double);
+static_assert(dz::kCounterWords * 4 <= kStaticOffGroupBegin, "work counters overflow their scratch slot");
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kStaticBytes];
+
 // Tiles of one size over all of a table's tensors, in device memory.
 struct ChunkList {
   uint32_t elems = 0;  // tile size (elements)
@@ -352,11 +373,39 @@ hipError_t upload_chunks(const std::vector<DzChunk>& v, DzChunk** d) {
   return e;
 }
 
+// The device address of `scratch` on device `dev` (current) and the device's
+// CU count, looked up once per device. In host code `scratch` names a host
+// stand-in, not device memory: the kernels get this address instead.
+struct StaticScratch {
+  bool ready = false;
+  unsigned char* ptr = nullptr;
+  int cus = 0;
+};
+std::mutex g_static_mu;
+StaticScratch g_static[kMaxDevices];
+
+int32_t static_scratch(int dev, StaticScratch** out) {
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  StaticScratch& s = g_static[dev];
+  if (!s.ready) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    e = hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
+    s.ptr = (unsigned char*)p;
+    s.ready = true;
+  }
+  *out = &s;
+  return DZ_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int32_t dz_version(void) { return 100; }
+// 2.0.0: z from Philox4x32-7 (1.0.0 used Philox4x32-10); dz_group_sumsq_static
+int32_t dz_version(void) { return 20000; }
 
 const char* dz_last_error(void) { return g_last_error.c_str(); }
 
@@ -594,6 +643,83 @@ int32_t dz_group_sumsq(dz_table* t, double* d_sumsq, float* d_norm_f32, void* d_
   }
   e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_sumsq, d_norm_f32,
                           d_norm_T, true, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
+  return DZ_OK;
+}
+
+int32_t dz_group_sumsq_static(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const int64_t* numels, int32_t n,
+                              int32_t dtype, double* d_sumsq, float* d_norm_f32, void* d_norm_T, void* stream) {
+  if (!ptrs || !anchor_ptrs || !numels) return fail(DZ_ERR_INVALID, "ptrs/anchor_ptrs/numels is NULL");
+  if (n <= 0 || (uint32_t)n > kStaticMaxGroups) {
+    return fail(DZ_ERR_INVALID, "group count must be in [1, " + std::to_string(kStaticMaxGroups) + "]");
+  }
+  if (!valid_dtype(dtype)) return fail(DZ_ERR_INVALID, "unknown dtype");
+  int dev;
+  int32_t rc = current_device(&dev);
+  if (rc) return rc;
+  const int es = elem_size(dtype);
+  uint64_t total = 0;
+  for (int32_t i = 0; i < n; ++i) {
+    if (numels[i] < 0) return fail(DZ_ERR_INVALID, "negative numel for tensor " + std::to_string(i));
+    total += ((uint64_t)numels[i] + dz::kProjChunk - 1) / dz::kProjChunk;
+  }
+  if (total > kStaticMaxChunks) {
+    return fail(DZ_ERR_INVALID, "the tensors make " + std::to_string(total) + " chunks of " +
+                                    std::to_string(dz::kProjChunk) + " elements; at most " +
+                                    std::to_string(kStaticMaxChunks) + " fit the static scratch");
+  }
+  for (int32_t i = 0; i < n; ++i) {
+    if (numels[i] > 0) {
+      rc = check_range(ptrs[i], (uint64_t)numels[i] * es, "theta", i);
+      if (!rc) rc = check_range(anchor_ptrs[i], (uint64_t)numels[i] * es, "anchor", i);
+      if (rc) return rc;
+    }
+  }
+  const uint64_t out_bytes[3] = {(uint64_t)n * 8, (uint64_t)n * 4, (uint64_t)n * es};
+  const void* outs[3] = {d_sumsq, d_norm_f32, d_norm_T};
+  const char* out_names[3] = {"sumsq", "norm_f32", "norm_T"};
+  for (int k = 0; k < 3; ++k) {
+    if (outs[k]) {
+      rc = check_range((uint64_t)(uintptr_t)outs[k], out_bytes[k], out_names[k], 0);
+      if (rc) return rc;
+    }
+  }
+  StaticScratch* sc = nullptr;
+  rc = static_scratch(dev, &sc);
+  if (rc) return rc;
+  uint32_t* counters = (uint32_t*)(sc->ptr + kStaticOffCounters);
+  uint32_t* group_begin = (uint32_t*)(sc->ptr + kStaticOffGroupBegin);
+  DzChunk* chunks = (DzChunk*)(sc->ptr + kStaticOffChunks);
+  double* partials = (double*)(sc->ptr + kStaticOffPartials);
+  const hipStream_t st = (hipStream_t)stream;
+  // the chunk plan, kStaticPlanGroups groups per launch (the group list travels as a kernel argument)
+  uint32_t next = 0;
+  for (int32_t g0 = 0; g0 < n; g0 += dz::kStaticPlanGroups) {
+    dz::StaticPlanBatch b{};
+    b.ngroups = (uint32_t)std::min<int32_t>(dz::kStaticPlanGroups, n - g0);
+    b.group_base = (uint32_t)g0;
+    b.total_groups = (uint32_t)n;
+    b.total_chunks = (uint32_t)total;
+    b.elem_size = es;
+    b.first = g0 == 0;
+    for (uint32_t k = 0; k < b.ngroups; ++k) {
+      b.ptr[k] = ptrs[g0 + k];
+      b.anchor[k] = anchor_ptrs[g0 + k];
+      b.numel[k] = numels[g0 + k];
+      b.chunk_begin[k] = next;
+      next += (uint32_t)(((uint64_t)numels[g0 + k] + dz::kProjChunk - 1) / dz::kProjChunk);
+    }
+    hipError_t e = dz::launch_static_plan(b, chunks, group_begin, counters, st);
+    if (e != hipSuccess) return hip_fail(e, "plan kernel launch");
+  }
+  if (total > 0) {
+    const uint32_t grid = std::min<uint32_t>((uint32_t)total, (uint32_t)DZ_PROJ_WG_PER_CU * (uint32_t)sc->cus);
+    hipError_t e = dz::launch_proj(dtype, dz::kProjSumsq, chunks, (uint32_t)total, (uint32_t)n, grid, nullptr,
+                                   partials, counters, st);
+    if (e != hipSuccess) return hip_fail(e, "sumsq kernel launch");
+  }
+  hipError_t e =
+      dz::launch_finalize(dtype, partials, group_begin, (uint32_t)n, d_sumsq, d_norm_f32, d_norm_T, true, st);
   if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
   return DZ_OK;
 }

@@ -131,6 +131,24 @@ hipError_t launch_dot(int dtype, const DzChunk* chunks, uint32_t nchunks, const 
 // take_sqrt: norms (sqrt of the sums) or plain sums in the fp32 / T outputs.
 hipError_t launch_finalize(int dtype, const double* partials, const uint32_t* gbegin, uint32_t ngroups,
                            double* sumsq, float* norm_f32, void* norm_T, bool take_sqrt, hipStream_t st);
+// Chunk plan of a projection launch without a table (dz_group_sumsq_static):
+// kStaticPlanGroups groups per plan launch, their descriptors and the
+// group -> chunk index written into caller-provided device memory.
+constexpr int kStaticPlanGroups = 64;
+struct StaticPlanBatch {
+  uint64_t ptr[kStaticPlanGroups];
+  uint64_t anchor[kStaticPlanGroups];
+  int64_t numel[kStaticPlanGroups];
+  uint32_t chunk_begin[kStaticPlanGroups];  // first chunk of each group of the batch
+  uint32_t ngroups;                         // groups in this batch
+  uint32_t group_base;                      // index of the batch's first group
+  uint32_t total_groups;
+  uint32_t total_chunks;
+  int32_t elem_size;
+  uint32_t first;  // the first batch also zeroes the work counters
+};
+hipError_t launch_static_plan(const StaticPlanBatch& b, DzChunk* chunks, uint32_t* group_begin, uint32_t* counters,
+                              hipStream_t st);
 hipError_t launch_normals(int dtype, const void* tab, uint64_t seed, uint32_t stream, uint64_t offset,
                           uint64_t n, void* out, hipStream_t st);
 hipError_t launch_philox(uint64_t seed, uint32_t stream, uint64_t q0, uint64_t n, uint32_t* out,

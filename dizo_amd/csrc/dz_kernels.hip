@@ -912,6 +912,42 @@ __global__ void __launch_bounds__(kProjThreads) finalize_kernel(const double* __
   }
 }
 
+// Chunk descriptors of a projection launch planned on the device (the
+// table-free norm pass): block g writes group g's chunks, split as
+// dz_table_create splits them (kProjChunk elements, the last one shorter;
+// aligned when theta and theta0 are 16-byte aligned), and its first chunk
+// index; the last batch also writes the end index of the last group. The
+// first batch zeroes the work counters the projection kernel takes chunks
+// from.
+__global__ void __launch_bounds__(256) static_plan_kernel(StaticPlanBatch b, DzChunk* __restrict__ chunks,
+                                                          uint32_t* __restrict__ group_begin,
+                                                          uint32_t* __restrict__ counters) {
+  const uint32_t g = blockIdx.x;
+  if (b.first && g == 0) {
+    for (int i = threadIdx.x; i < kCounterWords; i += blockDim.x) counters[i] = 0u;
+  }
+  if (g >= b.ngroups) return;
+  const uint32_t gi = b.group_base + g;
+  const uint64_t p = b.ptr[g], a = b.anchor[g];
+  const int64_t ne = b.numel[g];
+  const uint32_t meta = gi | ((p % 16 == 0 && a % 16 == 0) ? kDzMetaAligned : 0u);
+  const uint32_t nch = (uint32_t)((ne + kProjChunk - 1) / kProjChunk);
+  for (uint32_t k = threadIdx.x; k < nch; k += blockDim.x) {
+    const uint64_t s = (uint64_t)k * kProjChunk;
+    DzChunk c;
+    c.ptr = p + s * (uint64_t)b.elem_size;
+    c.aux = a + s * (uint64_t)b.elem_size;
+    c.zgroup = s;
+    c.n = (uint32_t)min((int64_t)kProjChunk, ne - (int64_t)s);
+    c.meta = meta;
+    chunks[b.chunk_begin[g] + k] = c;
+  }
+  if (threadIdx.x == 0) {
+    group_begin[gi] = b.chunk_begin[g];
+    if (gi + 1 == b.total_groups) group_begin[b.total_groups] = b.total_chunks;
+  }
+}
+
 // z(seed, stream, offset + i) for i < n, written densely in T.
 template <int DT>
 __global__ void __launch_bounds__(256) normals_kernel(const void* __restrict__ gtab, uint64_t seed,
@@ -1064,6 +1100,13 @@ hipError_t launch_finalize(int dtype, const double* partials, const uint32_t* gb
     default:
       return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_static_plan(const StaticPlanBatch& b, DzChunk* chunks, uint32_t* group_begin, uint32_t* counters,
+                              hipStream_t st) {
+  hipLaunchKernelGGL(static_plan_kernel, dim3(b.ngroups ? b.ngroups : 1), dim3(256), 0, st, b, chunks, group_begin,
+                     counters);
   return hipGetLastError();
 }
 

@@ -139,6 +139,21 @@ int32_t dz_philox(uint64_t seed, uint32_t stream_id, uint64_t q0, int64_t n, uin
 int32_t dz_group_sumsq(dz_table* t, double* d_sumsq, float* d_norm_f32, void* d_norm_T,
                        void* stream);
 
+/* dz_group_sumsq without a table and without allocating: no counterpart in
+ * the reference. For callers that cannot allocate device memory (code under
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The n
+ * groups are theta ptrs[g] with anchors anchor_ptrs[g], numels[g] elements of
+ * `dtype` each; the outputs are dz_group_sumsq's, bit for bit. Chunk
+ * descriptors, partial sums and work counters live in a static device array
+ * of the library (10.5 MB per device, held until the process ends): at most
+ * 4096 groups and 262,144 chunks of 32,768 elements (8.6 G elements); larger
+ * inputs return DZ_ERR_INVALID. Every call on one device shares that array,
+ * so calls that overlap in time on one device race: order them on one
+ * stream. */
+int32_t dz_group_sumsq_static(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const int64_t* numels,
+                              int32_t n, int32_t dtype, double* d_sumsq, float* d_norm_f32, void* d_norm_T,
+                              void* stream);
+
 /* mode DZ_PROJ_APPLY / DZ_PROJ_REVERSE / DZ_PROJ_REVERSE_SUMSQ with one alpha
  * per group (device array of the table dtype). APPLY replaces the copy_ of
  * apply_constraints (trainer.py:428-436); REVERSE replaces reverse_constraints
