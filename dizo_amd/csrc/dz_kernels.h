@@ -37,8 +37,10 @@ struct DzPtrArray {
 // MI355X at OPT-13B size (643 tensors, fp16): 64 KB tiles (four groups per
 // thread) and one workgroup per CU stream best for every mode: perturb 6.4
 // TB/s against 6.05 with 16 KB tiles and two workgroups per CU (which a 64 KB
-// table would allow), restore+update 6.4-6.5 TB/s. fp32 uses 64 KB tiles too
-// (two groups of 8 fp32 per thread). The macros let experiments build others.
+// table would allow), restore+update 6.4-6.5 TB/s. fp32 uses 32 KB tiles (one
+// group of 8 fp32 per thread): its only workload, OPT-125m (347 MB of
+// parameters, about 40 tiles per CU), runs a pass in 126 us that way against
+// 140 us with 64 KB tiles. The macros let experiments build others.
 #ifndef DZ_RMW_GROUPS_NARROW
 #define DZ_RMW_GROUPS_NARROW 4
 #endif
@@ -46,7 +48,7 @@ struct DzPtrArray {
 #define DZ_RMW_GROUPS_WIDE16 4
 #endif
 #ifndef DZ_RMW_GROUPS_WIDE32
-#define DZ_RMW_GROUPS_WIDE32 2
+#define DZ_RMW_GROUPS_WIDE32 1
 #endif
 #ifndef DZ_RMW_COUNTERS
 #define DZ_RMW_COUNTERS 8

@@ -159,10 +159,26 @@ __device__ __forceinline__ uint32_t table_entry(uint32_t qbits, const DzScalars&
 typedef _Float16 dz_half2 __attribute__((ext_vector_type(2)));
 typedef __bf16 dz_bf2 __attribute__((ext_vector_type(2)));
 
+// bf16 lanes of a packed word as fp32 (a bf16 value is the high half of its
+// fp32 bit pattern), and two fp32 values rounded to bf16 and packed by one
+// v_cvt_pk_bf16_f32 (round to nearest even, as torch converts fp32 to bf16).
+__device__ __forceinline__ float bf16_lo_f(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf16_hi_f(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  const dz_bf2 r = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, r);
+}
+// R_bf16(a + b) lane by lane for packed bf16 words, the fp32 sums written out.
+__device__ __forceinline__ uint32_t add_pair_bf16(uint32_t a, uint32_t b) {
+  return pack_bf16(bf16_lo_f(a) + bf16_lo_f(b), bf16_hi_f(a) + bf16_hi_f(b));
+}
+
 // R_T(a + b) for a pair of 16-bit values packed in one word: fp16 adds
 // natively (v_pk_add_f16); bf16 adds in fp32 and rounds both lanes with one
 // v_cvt_pk_bf16_f32 (RNE). Either equals the reference's fp32 add rounded
-// to T: fp32 holds at least 2p + 2 bits of a p-bit format.
+// to T: fp32 holds at least 2p + 2 bits of a p-bit format. (Written out for
+// bf16: the compiler's own bf16 vector add issued about 5 conversions per
+// three-add chain of a word instead of 3.)
 template <int DT>
 __device__ __forceinline__ uint32_t add_pair(uint32_t a, uint32_t b) {
   if constexpr (DT == DZ_F16) {
@@ -170,9 +186,7 @@ __device__ __forceinline__ uint32_t add_pair(uint32_t a, uint32_t b) {
     const dz_half2 y = __builtin_bit_cast(dz_half2, b);
     return __builtin_bit_cast(uint32_t, x + y);
   } else {
-    const dz_bf2 x = __builtin_bit_cast(dz_bf2, a);
-    const dz_bf2 y = __builtin_bit_cast(dz_bf2, b);
-    return __builtin_bit_cast(uint32_t, x + y);
+    return add_pair_bf16(a, b);
   }
 }
 
@@ -275,7 +289,8 @@ __device__ __forceinline__ uint32_t combine_pair16(uint32_t th, uint32_t w, uint
   if constexpr (!rmw_pair_mode(MODE)) {
     return add_pair<DT>(th, (t.e0 | (t.e1 << 16)) ^ sw);
   } else {
-    // entry = b | (-d) << 16 for a positive z
+    // entry = b | (-d) << 16 for a positive z (bf16 here: the fp16 pair modes
+    // return above)
     const uint32_t b = pack_lo(t.e0, t.e1) ^ sw;
     const uint32_t nd = pack_hi(t.e0, t.e1) ^ sw;
     uint32_t r = add_pair<DT>(add_pair<DT>(th, b), nd);

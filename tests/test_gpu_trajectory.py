@@ -433,3 +433,57 @@ def test_c4_opt13b_fp16_passes_and_projection():
     want = torch.stack([_lib_norm(th[i] - t0[i]) for i in gs])
     assert _same(norms[gs], want)
     ptab.close()
+
+
+def _fingerprints(model) -> torch.Tensor:
+    """One exact integer per parameter: the sum of its bit patterns weighted by
+    (position mod 1021) + 1, in int64 (any differing element changes it unless
+    the changes cancel in that weighted sum)."""
+    out = []
+    with torch.no_grad():
+        for p in model.parameters():
+            bits = _bits(p.data).reshape(-1).to(torch.int64)
+            w = torch.arange(bits.numel(), device=bits.device, dtype=torch.int64) % 1021 + 1
+            out.append((bits * w).sum())
+            del bits, w
+    return torch.stack(out).cpu()
+
+
+def test_c5_opt30b_bf16_graph_replay_matches_eager():
+    """Config C5's captured-graph replay (OPT-30B bf16, batch 8 x 2 candidates of
+    256 tokens, the 96 projected groups' anchors on the device; the bench's
+    forward: fused decoder-layer GEMMs, option-position head, SDPA): four ZO
+    steps with the DiZO event (10 SPSA iterations, trainer.py:782-803) after
+    the second, run eagerly and replayed from captured graphs. The losses and
+    every one of the 771 trainable tensors (by exact fingerprint) agree bit
+    for bit."""
+    import gc
+
+    from dizo_amd.synth import Cycle, build_opt, make_batches
+    from dizo_amd.trainer import ZOArguments, ZOTrainer
+    batches = make_batches(2, 8, 50272, seed=9, device="cuda", fixed_len=256)
+
+    def run(graph: bool):
+        model = build_opt("opt-30b", torch.bfloat16, "cuda", seed=0)
+        args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=100, enhanced="zo", zo_graph=graph,
+                           zo_option_head=True, zo_fused_mlp=True, zo_fused_qkv=True)
+        np.random.seed(26)
+        tr = ZOTrainer(model, args, train_dataloader=Cycle(batches))
+        tr.state.global_step = 48  # the event follows the update of global step 49, the second step
+        it = iter(Cycle(batches))
+        losses = torch.stack([tr.training_step(next(it)).reshape(()).float() for _ in range(4)])
+        tr.zo_close()
+        torch.cuda.synchronize()
+        assert tr.dizo_trainer.i == 1
+        fp = _fingerprints(model)
+        out = (losses.cpu(), fp, len(list(model.parameters())))
+        del tr, model
+        gc.collect()
+        torch.cuda.empty_cache()
+        return out
+
+    le, fe, n = run(False)
+    lg, fg, _ = run(True)
+    assert n >= 771
+    assert torch.equal(le, lg), f"losses {le.tolist()} vs {lg.tolist()}"
+    assert torch.equal(fe, fg), f"{int((fe != fg).sum())} tensors differ"
