@@ -35,7 +35,7 @@ the whole step at C1, a sampled and scaled step otherwise.
 
   python bench.py [--gpus 1] [--steps 50] [--warmup 3] [--workload c4] [--graph] [--full-logits] [--hf-layers]
                   [--dz-attention]
-  python bench.py --kernels [--workload c4]     # per-pass kernel microbench (config C2 style)
+  python bench.py --kernels [--workload c2|c4]  # per-pass kernel microbench (config C2: OPT-2.7B fp16)
 """
 from __future__ import annotations
 
@@ -54,6 +54,9 @@ HBM_PEAK_GBPS = 8000.0
 WORKLOADS = {
     # BASELINE.json configs; c4 is the one the metric is quoted on
     "c1": dict(shape="opt-125m", dtype="float32", batch=16, min_len=32, max_len=64, fixed_len=None),
+    # C2 is kernel-only (--kernels): the ZO passes over OPT-2.7B's fp16 trainable set
+    "c2": dict(shape="opt-2.7b", dtype="float16", batch=16, min_len=32, max_len=64, fixed_len=None,
+               kernels_only=True),
     "c3": dict(shape="opt-2.7b", dtype="float16", batch=16, min_len=32, max_len=64, fixed_len=None),
     "c4": dict(shape="opt-13b", dtype="float16", batch=16, min_len=None, max_len=None, fixed_len=128),
     "c5": dict(shape="opt-30b", dtype="bfloat16", batch=8, min_len=None, max_len=None, fixed_len=256),
@@ -534,7 +537,13 @@ def kernel_microbench(wl_name: str, reps: int = 10, log=print):
     t = float(np.median(ms))
     out["device_copy_4GiB"] = {"ms": t, "GBps": 2 * copy_bytes / t / 1e6, "frac": 2 * copy_bytes / t / 1e6 / HBM_PEAK_GBPS}
     log(f"[kernels] device copy 4 GiB {t:8.3f} ms {2 * copy_bytes / t / 1e6:8.1f} GB/s")
-    return {"bytes_per_pass": nbytes, "passes": out, "calibration_copy_bytes": copy_bytes}
+    eb = torch.finfo(dtype).bits // 8
+    # one ZO step of the reference (trainer.py:1580-1608): +1, -2, +1 and the update, 4 read-modify-write
+    # passes; fused: +1, -2 and restore+update (3); across steps: -2 and restore+update+next perturb (2)
+    steps = {"separate": 4, "restore_update_fused": 3, "next_perturb_fused": 2}
+    return {"bytes_per_pass": nbytes, "passes": out, "calibration_copy_bytes": copy_bytes,
+            "launches_per_step": steps,
+            "bytes_per_param_per_step": {k: 2 * eb * v for k, v in steps.items()}}
 
 
 def main(argv=None):
@@ -577,6 +586,9 @@ def main(argv=None):
     from dizo_amd import _lib
 
     _lib.load()
+    if WORKLOADS[a.workload].get("kernels_only") and not a.kernels:
+        print(json.dumps({"error": f"workload {a.workload} is a kernel microbench: add --kernels"}), flush=True)
+        return 2
     if a.kernels:
         res = kernel_microbench(a.workload, log=log)
         line = {"metric": "ZO pass HBM GB/s", "workload": a.workload, **res}

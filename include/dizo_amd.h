@@ -173,10 +173,13 @@ int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sum
 int32_t dz_group_dot(dz_table* t, const uint64_t* other_ptrs, double* d_dot, float* d_dot_f32,
                      void* stream);
 
-/* Causal self-attention of an unpadded batch, for the ZO step's forwards: the
- * SDPA call of HF's OPTAttention.forward when no mask is given (is_causal), as
- * reached from the reference's model call in forward_wrap_with_option_len
- * (trainer.py:1464). dtype DZ_DTYPE_F16 or DZ_DTYPE_BF16; head_dim 64 or 128;
+/* Causal self-attention of an unpadded batch, for the ZO step's forwards. No
+ * counterpart in the reference: it replaces the SDPA call inside HF
+ * transformers' OPTAttention.forward when no mask is given (is_causal), a
+ * library the reference calls from its model forward. Not bit for bit with
+ * SDPA (within its rounding), so the step's loss trajectory drifts from the
+ * SDPA one; the trainer uses it only when asked (zo_fused_attention).
+ * dtype DZ_DTYPE_F16 or DZ_DTYPE_BF16; head_dim 64 or 128;
  * L a multiple of 32 in [32, 256]. Element offsets: token t of sequence b,
  * head h of q starts at q + b * q_seq + t * q_tok + h * head_dim (k and v
  * alike); pointers and strides 16-byte aligned. q is used as R_T(q * scale)

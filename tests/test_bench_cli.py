@@ -35,10 +35,32 @@ def test_no_gpu_reports_an_error_line(capsys):
 
 
 def test_flags_and_workloads():
-    assert set(bench.WORKLOADS) == {"c1", "c3", "c4", "c5"}
+    assert set(bench.WORKLOADS) == {"c1", "c2", "c3", "c4", "c5"}
+    assert bench.WORKLOADS["c2"]["kernels_only"] and bench.WORKLOADS["c2"]["shape"] == "opt-2.7b"
     c4 = bench.WORKLOADS["c4"]
     assert (c4["shape"], c4["dtype"], c4["batch"], c4["fixed_len"]) == ("opt-13b", "float16", 16, 128)
     for flags in (["--graph"], ["--full-logits"], ["--hf-layers"], ["--sdpa"], ["--dz-attention"], ["--kernels"],
                   ["--enhanced", "fo"],
-                  ["--workload", "c5"], ["--no-cpu-baseline"]):
+                  ["--workload", "c5"], ["--workload", "c2", "--kernels"], ["--no-cpu-baseline"]):
         assert bench.main(flags + ["--gpus", "3"]) == 2  # parses, then stops at the one-GPU check
+
+
+def test_event_lands_in_every_timed_window():
+    """The step counter offset puts the DiZO event (after the update of every
+    50th step) on timed step min(steps, 50) - 1, whatever the warm-up."""
+    for steps in (1, 5, 20, 49, 50, 51, 120):
+        for warmup in (0, 1, 3, 5, 49, 50, 77):
+            off = bench.event_offset(steps, warmup)
+            timed = [off + warmup + j for j in range(steps)]
+            events = [j for j, g in enumerate(timed) if (g + 1) % 50 == 0]
+            assert events and events[0] == min(steps, 50) - 1, (steps, warmup, off, events)
+
+
+def test_amortised_rate():
+    # 20 steps in 5 s of which one 2 s event: 3 s of steps; one event per 50 steps adds 2 * 20 / 50 = 0.8 s
+    v, zo, ev = bench.amortised(20, 5.0, [2.0])
+    assert abs(v - 20 / 3.8) < 1e-12 and abs(zo - 20 / 3.0) < 1e-12 and ev == 2.0
+    # 50 steps with one event: the plain rate
+    v, _, _ = bench.amortised(50, 10.0, [2.0])
+    assert abs(v - 5.0) < 1e-12
+    assert bench.amortised(10, 2.0, []) == (5.0, 5.0, None)
