@@ -28,8 +28,11 @@ for bit, so its loss trajectory drifts from SDPA's: opt-in).
 
 Prints one JSON line. `roofline` is the dominant library kernel (the
 multi-tensor perturb / restore+update read-modify-write): algorithmic bytes
-2*b*P per launch over its mean device time, measured with stream events
-around every launch in the timed region. `cpu_baseline` times the
+2*b*P per launch over its mean device time, measured for every launch in the
+timed region with a stream-event pair that the runtime records as the kernel
+starts and ends (hipExtLaunchKernel, through dz_table_time_next), so the
+host's launch work is not counted; the rocprofv3 kernel trace of the same
+command agrees with it. `cpu_baseline` times the
 reference's expressions (the oracle's torch restatement) on the host cores:
 the whole step at C1, a sampled and scaled step otherwise.
 
@@ -417,6 +420,7 @@ def kernel_microbench(wl_name: str, reps: int = 10, log=print):
     import torch
 
     from dizo_amd.synth import SHAPES, build_opt
+    from dizo_amd.timing import KernelTimer
     from dizo_amd.trainer import _ZOTables, select_trainable
 
     wl = WORKLOADS[wl_name]
@@ -435,20 +439,19 @@ def kernel_microbench(wl_name: str, reps: int = 10, log=print):
         "restore_update": lambda t: t.restore_update(26, 1e-3, g, 1e-6),
         "restore_update_perturb": lambda t: t.restore_update_perturb(26, 27, 1e-3, g, 1e-6),
     }
+    # each launch timed from its first kernel's start to its last kernel's end (KernelTimer with tables)
+    timer = KernelTimer()
+    zo_tables = [tab for tab, _ in tabs.tables]
     for name, fn in cases.items():
-        for tab, _ in tabs.tables:
+        for tab in zo_tables:
             fn(tab)
         torch.cuda.synchronize()
-        ms = []
         for _ in range(reps):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for tab, _ in tabs.tables:
-                fn(tab)
-            e1.record()
+            with timer.span(name, nbytes, zo_tables):
+                for tab in zo_tables:
+                    fn(tab)
             torch.cuda.synchronize()
-            ms.append(e0.elapsed_time(e1))
-        t = float(np.median(ms))
+        t = float(np.median([a.elapsed_time(b) for a, b, _ in timer.spans[name]]))
         out[name] = {"ms": t, "GBps": nbytes / t / 1e6, "frac": nbytes / t / 1e6 / HBM_PEAK_GBPS}
         log(f"[kernels] {name:15s} {t:8.3f} ms {nbytes / t / 1e6:8.1f} GB/s")
     tabs.close()
@@ -475,15 +478,11 @@ def kernel_microbench(wl_name: str, reps: int = 10, log=print):
     for name, (k, fn) in proj_cases.items():
         fn()
         torch.cuda.synchronize()
-        ms = []
         for _ in range(reps):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            fn()
-            e1.record()
+            with timer.span(name, k * pbytes, [ptab]):
+                fn()
             torch.cuda.synchronize()
-            ms.append(e0.elapsed_time(e1))
-        t = float(np.median(ms))
+        t = float(np.median([a.elapsed_time(b) for a, b, _ in timer.spans[name]]))
         nb = k * pbytes
         out[name] = {"ms": t, "GBps": nb / t / 1e6, "frac": nb / t / 1e6 / HBM_PEAK_GBPS, "bytes": nb}
         log(f"[kernels] {name:15s} {t:8.3f} ms {nb / t / 1e6:8.1f} GB/s")
@@ -655,6 +654,7 @@ def main(argv=None):
             "traffic": load_traffic("rmw_kernel", a.workload),
             "algorithmic_bytes_per_launch": dom["bytes_per_launch"] if dom else None,
             "mean_launch_ms": dom["mean_ms"] if dom else None,
+            "launch_timing": "kernel start/end events (hipExtLaunchKernel)",
             # all read-modify-write launches of the window together
             "rmw_all": {"GBps": rmw_bytes / (rmw_ms * 1e-3) / 1e9 if rmw_ms else None,
                         "frac": rmw_bytes / (rmw_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS if rmw_ms else None,

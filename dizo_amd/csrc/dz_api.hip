@@ -229,9 +229,17 @@ struct dz_table {
   double* d_partials = nullptr;
   uint32_t* d_counters = nullptr;  // work counters of the persistent RMW / projection kernels
   DeviceState* dev = nullptr;
+  dz::LaunchEvents timing;  // dz_table_time_next's request for the next launching call
 };
 
 namespace {
+
+// The table's pending timing request, taken (and cleared) by a launching call.
+dz::LaunchEvents take_timing(dz_table* t) {
+  const dz::LaunchEvents ev = t->timing;
+  t->timing = dz::LaunchEvents{};
+  return ev;
+}
 
 int32_t check_table(const dz_table* t) {
   if (!t) return fail(DZ_ERR_INVALID, "table is NULL");
@@ -284,6 +292,7 @@ uint32_t proj_grid(const dz_table* t) {
 int32_t rmw(dz_table* t, int mode, const dz::DzScalars& s, const dz::DzScalarPtrs& p, void* stream) {
   int32_t rc = check_table(t);
   if (rc) return rc;
+  const dz::LaunchEvents ev = take_timing(t);
   if (t->projection) return fail(DZ_ERR_INVALID, "perturb/update need a ZO table (created without anchors)");
   const uint32_t want = (uint32_t)dz::rmw_chunk_elems(t->dtype, mode);
   const DzChunk* chunks = t->d_chunks;
@@ -295,7 +304,7 @@ int32_t rmw(dz_table* t, int mode, const dz::DzScalars& s, const dz::DzScalarPtr
   }
   if (ntiles == 0) return DZ_OK;
   hipError_t e = dz::launch_rmw(t->dtype, mode, chunks, ntiles, rmw_grid(t, mode, ntiles),
-                                t->dev->tab[t->dtype], s, p, t->d_counters, (hipStream_t)stream);
+                                t->dev->tab[t->dtype], s, p, t->d_counters, (hipStream_t)stream, ev);
   if (e != hipSuccess) return hip_fail(e, "rmw kernel launch");
   return DZ_OK;
 }
@@ -563,6 +572,14 @@ int32_t dz_table_z_offset(const dz_table* t, int32_t idx, uint64_t* out) {
   return DZ_OK;
 }
 
+int32_t dz_table_time_next(dz_table* t, void* start_event, void* stop_event) {
+  int32_t rc = check_table(t);
+  if (rc) return rc;
+  t->timing.start = (hipEvent_t)start_event;
+  t->timing.stop = (hipEvent_t)stop_event;
+  return DZ_OK;
+}
+
 int32_t dz_perturb(dz_table* t, uint64_t seed, float scale, float eps, const uint64_t* d_seed, void* stream) {
   dz::DzScalars s{seed, 0, scale, eps, 0.0f, 0.0f};
   dz::DzScalarPtrs p{d_seed, nullptr, nullptr, nullptr};
@@ -632,17 +649,19 @@ int32_t dz_philox(uint64_t seed, uint32_t stream_id, uint64_t q0, int64_t n, uin
 int32_t dz_group_sumsq(dz_table* t, double* d_sumsq, float* d_norm_f32, void* d_norm_T, void* stream) {
   int32_t rc = check_table(t);
   if (rc) return rc;
+  dz::LaunchEvents ev = take_timing(t);
   if (!t->projection) return fail(DZ_ERR_INVALID, "group_sumsq needs a projection table");
   rc = check_group_outputs(t, d_sumsq, d_norm_f32, d_norm_T);
   if (rc) return rc;
   hipError_t e = hipSuccess;
   if (t->nchunks > 0) {
     e = dz::launch_proj(t->dtype, dz::kProjSumsq, t->d_chunks, t->nchunks, (uint32_t)t->n, proj_grid(t),
-                        nullptr, t->d_partials, t->d_counters, (hipStream_t)stream);
+                        nullptr, t->d_partials, t->d_counters, (hipStream_t)stream, {ev.start, nullptr});
     if (e != hipSuccess) return hip_fail(e, "sumsq kernel launch");
+    ev.start = nullptr;
   }
   e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_sumsq, d_norm_f32,
-                          d_norm_T, true, (hipStream_t)stream);
+                          d_norm_T, true, (hipStream_t)stream, ev);
   if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
   return DZ_OK;
 }
@@ -728,6 +747,7 @@ int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sum
                    void* d_norm_T, void* stream) {
   int32_t rc = check_table(t);
   if (rc) return rc;
+  dz::LaunchEvents ev = take_timing(t);
   if (!t->projection) return fail(DZ_ERR_INVALID, "project needs a projection table");
   if (mode != DZ_PROJ_APPLY && mode != DZ_PROJ_REVERSE && mode != DZ_PROJ_REVERSE_SUMSQ &&
       mode != DZ_PROJ_APPLY_F32ALPHA)
@@ -736,14 +756,17 @@ int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sum
   rc = check_range((uint64_t)(uintptr_t)d_alpha, (uint64_t)t->n * alpha_size, "alpha", 0);
   if (!rc) rc = check_group_outputs(t, d_sumsq, d_norm_f32, d_norm_T);
   if (rc) return rc;
+  const bool finalize = mode == DZ_PROJ_REVERSE_SUMSQ;
   if (t->nchunks > 0) {
     hipError_t e = dz::launch_proj(t->dtype, mode, t->d_chunks, t->nchunks, (uint32_t)t->n, proj_grid(t),
-                                   d_alpha, t->d_partials, t->d_counters, (hipStream_t)stream);
+                                   d_alpha, t->d_partials, t->d_counters, (hipStream_t)stream,
+                                   {ev.start, finalize ? nullptr : ev.stop});
     if (e != hipSuccess) return hip_fail(e, "projection kernel launch");
+    ev.start = nullptr;
   }
-  if (mode == DZ_PROJ_REVERSE_SUMSQ) {
+  if (finalize) {
     hipError_t e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_sumsq,
-                                       d_norm_f32, d_norm_T, true, (hipStream_t)stream);
+                                       d_norm_f32, d_norm_T, true, (hipStream_t)stream, ev);
     if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
   }
   return DZ_OK;
@@ -752,6 +775,7 @@ int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sum
 int32_t dz_group_dot(dz_table* t, const uint64_t* other_ptrs, double* d_dot, float* d_dot_f32, void* stream) {
   int32_t rc = check_table(t);
   if (rc) return rc;
+  dz::LaunchEvents ev = take_timing(t);
   if (!t->projection) return fail(DZ_ERR_INVALID, "group_dot needs a projection table");
   if (!other_ptrs) return fail(DZ_ERR_INVALID, "other_ptrs is NULL");
   for (int32_t i = 0; i < t->n; ++i) {
@@ -771,11 +795,12 @@ int32_t dz_group_dot(dz_table* t, const uint64_t* other_ptrs, double* d_dot, flo
     dz::DzPtrArray other{};
     for (int32_t i = g0; i < g1; ++i) other.p[i - g0] = other_ptrs[i];
     e = dz::launch_dot(t->dtype, t->d_chunks + c0, c1 - c0, other, (uint32_t)g0, t->d_partials + c0,
-                       (hipStream_t)stream);
+                       (hipStream_t)stream, {ev.start, nullptr});
     if (e != hipSuccess) return hip_fail(e, "dot kernel launch");
+    ev.start = nullptr;
   }
   e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_dot, d_dot_f32, nullptr,
-                          false, (hipStream_t)stream);
+                          false, (hipStream_t)stream, ev);
   if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
   return DZ_OK;
 }

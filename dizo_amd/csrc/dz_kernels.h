@@ -119,20 +119,30 @@ struct DzScalarPtrs {
   const float* lr;       // device fp32
 };
 
+// Timing events of one launch: when set, the runtime records `start` as the
+// kernel starts and `stop` as it ends (hipExtLaunchKernel), so an event pair
+// brackets the kernel itself rather than the host's launch work as well.
+struct LaunchEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+
 hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
                       const void* qtab, const DzScalars& s, const DzScalarPtrs& p, uint32_t* counters,
-                      hipStream_t st);
+                      hipStream_t st, const LaunchEvents& ev = {});
 // Persistent: `grid` workgroups share the chunks through `counters` (zero
 // before the launch; the launch leaves them at zero).
 hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t ngroups,
-                       uint32_t grid, const void* alpha, double* partials, uint32_t* counters, hipStream_t st);
+                       uint32_t grid, const void* alpha, double* partials, uint32_t* counters, hipStream_t st,
+                       const LaunchEvents& ev = {});
 // Chunks of groups group_base .. group_base + kMaxDotGroups - 1; other.p[i]
 // is the tensor of group group_base + i.
 hipError_t launch_dot(int dtype, const DzChunk* chunks, uint32_t nchunks, const DzPtrArray& other,
-                      uint32_t group_base, double* partials, hipStream_t st);
+                      uint32_t group_base, double* partials, hipStream_t st, const LaunchEvents& ev = {});
 // take_sqrt: norms (sqrt of the sums) or plain sums in the fp32 / T outputs.
 hipError_t launch_finalize(int dtype, const double* partials, const uint32_t* gbegin, uint32_t ngroups,
-                           double* sumsq, float* norm_f32, void* norm_T, bool take_sqrt, hipStream_t st);
+                           double* sumsq, float* norm_f32, void* norm_T, bool take_sqrt, hipStream_t st,
+                           const LaunchEvents& ev = {});
 // Chunk plan of a projection launch without a table (dz_group_sumsq_static):
 // kStaticPlanGroups groups per plan launch, their descriptors and the
 // group -> chunk index written into caller-provided device memory.

@@ -7,6 +7,7 @@
 // -ffp-contract=off and the pragma below), and dz_opq() keeps the backend from
 // folding an fp32 multiply and its fp16 conversion into one mixed-precision
 // FMA (which would round once instead of twice and flip the sign of zeros).
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -153,6 +154,57 @@ __device__ __forceinline__ uint32_t table_entry(uint32_t qbits, const DzScalars&
     return qbits;  // restore+update(+perturb) in fp32: z itself
   } else {
     return DT_<DT>::from_f(b) | ((DT_<DT>::from_f(d) ^ kSign) << 16);
+  }
+}
+
+typedef uint32_t dz_u32x4 __attribute__((ext_vector_type(4)));
+
+// The launch's delta table, built by the 1024 threads of a workgroup in two
+// steps: each thread loads its 16-byte slices of Q_T (4 fp32 or 8 16-bit
+// entries; slice t + v * 1024), all loads in flight at once (load_table), then
+// writes the slices' entries to the same indices of the LDS table
+// (store_table). A plain loop of one 32-bit load, a wait and one LDS store
+// per entry costs 32 memory latencies in a row per launch.
+template <int DT>
+struct TableSlices {
+  static constexpr int kPer = DT == DZ_F32 ? 4 : 8;  // Q_T entries per 16-byte slice
+  static constexpr int kSlices = kDzTabEntries / (kRmwThreads * kPer);
+  static_assert(kSlices * kRmwThreads * kPer == kDzTabEntries, "table slices");
+  dz_u32x4 q[kSlices];
+};
+
+template <int DT>
+__device__ __forceinline__ void load_table(TableSlices<DT>& t, const void* qtab) {
+#pragma unroll
+  for (int v = 0; v < TableSlices<DT>::kSlices; ++v)
+    t.q[v] = *(const dz_u32x4*)((const char*)qtab + (size_t)(v * kRmwThreads + threadIdx.x) * 16);
+}
+
+template <int DT, int MODE>
+__device__ __forceinline__ void store_table(typename RmwTraits<DT, MODE>::E* tab, const TableSlices<DT>& t,
+                                            const DzScalars& sc) {
+  using E = typename RmwTraits<DT, MODE>::E;
+  constexpr int kPer = TableSlices<DT>::kPer;
+#pragma unroll
+  for (int v = 0; v < TableSlices<DT>::kSlices; ++v) {
+    uint32_t e[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const uint32_t w = t.q[v][kPer == 4 ? i : i >> 1];
+      const uint32_t qb = kPer == 4 ? w : (i & 1 ? w >> 16 : w & 0xffffu);
+      e[i] = table_entry<DT, MODE>(qb, sc);
+    }
+    E* dst = tab + (size_t)(v * kRmwThreads + threadIdx.x) * kPer;
+    if constexpr (sizeof(E) == 4) {
+#pragma unroll
+      for (int h = 0; h < kPer / 4; ++h) {
+        const dz_u32x4 o = {e[4 * h], e[4 * h + 1], e[4 * h + 2], e[4 * h + 3]};
+        *(dz_u32x4*)(dst + 4 * h) = o;
+      }
+    } else {
+      const dz_u32x4 o = {e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
+      *(dz_u32x4*)dst = o;
+    }
   }
 }
 
@@ -331,8 +383,6 @@ __device__ __forceinline__ uint32_t apply_one(uint32_t th, uint32_t h, uint32_t 
     return r;
   }
 }
-
-typedef uint32_t dz_u32x4 __attribute__((ext_vector_type(4)));
 
 // Streaming 16-byte accesses: theta is touched once per pass, so loads and
 // stores carry the non-temporal hint. The pointers are global-memory ones
@@ -534,17 +584,11 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
                                                           uint32_t* __restrict__ counters) {
   using Tr = RmwTraits<DT, MODE>;
   using E = typename Tr::E;
-  using S = typename DT_<DT>::S;
   __shared__ __attribute__((aligned(16))) E tab[kDzTabEntries];
   // Tile bookkeeping rings: indices of tiles k .. k+3, descriptors of k .. k+2.
   __shared__ uint32_t sidx[4];
   __shared__ DzChunk sdesc[3];
   const DzScalars sc = resolve_scalars<DT>(sc_in, sp);
-  {
-    const S* q = (const S*)qtab;
-    for (int i = threadIdx.x; i < kDzTabEntries; i += kRmwThreads)
-      tab[i] = (E)table_entry<DT, MODE>((uint32_t)q[i], sc);
-  }
   // Counters in use: every one of them must be served by at least one
   // workgroup, or its tiles would never be taken (a small grid uses fewer).
   const uint32_t ncnt = rfl_u32(max(1u, min((uint32_t)kCounters, gridDim.x >> 3)));
@@ -555,16 +599,28 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
   // taken from the counter and the descriptor of tile k+2 is loaded, so
   // neither latency sits between two tiles. A tile's data is loaded when its
   // turn comes: loading tile k + 1 during tile k measured slower for every
-  // mode once the three-way pass's ALU work had shrunk.
+  // mode (16-bit at OPT-13B, fp32 at OPT-125m). Start-up: lane 0 takes the
+  // first three tickets with one atomic, the table's loads are issued behind
+  // it, then the first two descriptors are loaded (clamped to a valid index;
+  // only tickets below nchunks are used) and the table is written.
+  uint32_t t0 = 0;
+  if (threadIdx.x == 0) t0 = atomicAdd(mine, 3u);
+  TableSlices<DT> qs;
+  load_table<DT>(qs, qtab);
   if (threadIdx.x == 0) {
     uint64_t c[3];
     for (int i = 0; i < 3; ++i) {
-      c[i] = (uint64_t)atomicAdd(mine, 1u) * ncnt + j;
+      c[i] = (uint64_t)(t0 + i) * ncnt + j;
       sidx[i] = (uint32_t)min(c[i], nch);
     }
-    if (c[0] < nch) sdesc[0] = chunks[c[0]];
-    if (c[1] < nch) sdesc[1] = chunks[c[1]];
+    if (nch > 0) {
+      const DzChunk d0 = chunks[min(c[0], nch - 1)];
+      const DzChunk d1 = chunks[min(c[1], nch - 1)];
+      sdesc[0] = d0;
+      sdesc[1] = d1;
+    }
   }
+  store_table<DT, MODE>(tab, qs, sc);
   __syncthreads();
   TileRegs<DT, MODE> cur;
   for (uint32_t k = 0;; ++k) {
@@ -993,27 +1049,38 @@ __global__ void __launch_bounds__(256) philox_kernel(uint64_t seed, uint32_t str
 
 // ---------------------------------------------------------------------------
 // Launchers (host side, C++ linkage; the C ABI validates before calling).
+// With timing events given (LaunchEvents), a launch goes through
+// hipExtLaunchKernel, which records them when the kernel starts and ends.
 // ---------------------------------------------------------------------------
+#define DZ_LAUNCH(kernel, grid, block, st, ev, ...)                                              \
+  do {                                                                                          \
+    if ((ev).start || (ev).stop) {                                                              \
+      hipExtLaunchKernelGGL(kernel, grid, block, 0, st, (ev).start, (ev).stop, 0, __VA_ARGS__); \
+    } else {                                                                                    \
+      hipLaunchKernelGGL(kernel, grid, block, 0, st, __VA_ARGS__);                              \
+    }                                                                                           \
+  } while (0)
+
 template <int DT>
 static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
                                 const void* tab, const DzScalars& s, const DzScalarPtrs& p,
-                                uint32_t* counters, hipStream_t st) {
+                                uint32_t* counters, hipStream_t st, const LaunchEvents& ev) {
   switch (mode) {
     case kModePerturb:
-      hipLaunchKernelGGL((rmw_kernel<DT, kModePerturb>), dim3(grid), dim3(kRmwThreads), 0, st,
+      DZ_LAUNCH((rmw_kernel<DT, kModePerturb>), dim3(grid), dim3(kRmwThreads), st, ev,
                          chunks, nchunks, tab, s, p, counters);
       break;
     case kModeUpdate:
-      hipLaunchKernelGGL((rmw_kernel<DT, kModeUpdate>), dim3(grid), dim3(kRmwThreads), 0, st,
+      DZ_LAUNCH((rmw_kernel<DT, kModeUpdate>), dim3(grid), dim3(kRmwThreads), st, ev,
                          chunks, nchunks, tab, s, p, counters);
       break;
     case kModeRestoreUpdate:
-      hipLaunchKernelGGL((rmw_kernel<DT, kModeRestoreUpdate>), dim3(grid), dim3(kRmwThreads), 0,
-                         st, chunks, nchunks, tab, s, p, counters);
+      DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdate>), dim3(grid), dim3(kRmwThreads),
+                         st, ev, chunks, nchunks, tab, s, p, counters);
       break;
     case kModeRestoreUpdatePerturb:
-      hipLaunchKernelGGL((rmw_kernel<DT, kModeRestoreUpdatePerturb>), dim3(grid), dim3(kRmwThreads), 0,
-                         st, chunks, nchunks, tab, s, p, counters);
+      DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdatePerturb>), dim3(grid), dim3(kRmwThreads),
+                         st, ev, chunks, nchunks, tab, s, p, counters);
       break;
     default:
       return hipErrorInvalidValue;
@@ -1023,11 +1090,11 @@ static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunk
 
 hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
                       const void* tab, const DzScalars& s, const DzScalarPtrs& p, uint32_t* counters,
-                      hipStream_t st) {
+                      hipStream_t st, const LaunchEvents& ev) {
   switch (dtype) {
-    case DZ_F32: return launch_rmw_dt<DZ_F32>(mode, chunks, nchunks, grid, tab, s, p, counters, st);
-    case DZ_F16: return launch_rmw_dt<DZ_F16>(mode, chunks, nchunks, grid, tab, s, p, counters, st);
-    case DZ_BF16: return launch_rmw_dt<DZ_BF16>(mode, chunks, nchunks, grid, tab, s, p, counters, st);
+    case DZ_F32: return launch_rmw_dt<DZ_F32>(mode, chunks, nchunks, grid, tab, s, p, counters, st, ev);
+    case DZ_F16: return launch_rmw_dt<DZ_F16>(mode, chunks, nchunks, grid, tab, s, p, counters, st, ev);
+    case DZ_BF16: return launch_rmw_dt<DZ_BF16>(mode, chunks, nchunks, grid, tab, s, p, counters, st, ev);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1035,26 +1102,26 @@ hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchun
 template <int DT>
 static hipError_t launch_proj_dt(int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t ngroups,
                                  uint32_t grid, const void* alpha, double* partials, uint32_t* counters,
-                                 hipStream_t st) {
+                                 hipStream_t st, const LaunchEvents& ev) {
   switch (mode) {
     case kProjSumsq:
-      hipLaunchKernelGGL((proj_kernel<DT, kProjSumsq>), dim3(grid), dim3(kProjThreads), 0, st, chunks, nchunks,
+      DZ_LAUNCH((proj_kernel<DT, kProjSumsq>), dim3(grid), dim3(kProjThreads), st, ev, chunks, nchunks,
                          ngroups, alpha, partials, counters);
       break;
     case kProjApply:
-      hipLaunchKernelGGL((proj_kernel<DT, kProjApply>), dim3(grid), dim3(kProjThreads), 0, st, chunks, nchunks,
+      DZ_LAUNCH((proj_kernel<DT, kProjApply>), dim3(grid), dim3(kProjThreads), st, ev, chunks, nchunks,
                          ngroups, alpha, partials, counters);
       break;
     case kProjReverse:
-      hipLaunchKernelGGL((proj_kernel<DT, kProjReverse>), dim3(grid), dim3(kProjThreads), 0, st, chunks, nchunks,
+      DZ_LAUNCH((proj_kernel<DT, kProjReverse>), dim3(grid), dim3(kProjThreads), st, ev, chunks, nchunks,
                          ngroups, alpha, partials, counters);
       break;
     case kProjReverseSumsq:
-      hipLaunchKernelGGL((proj_kernel<DT, kProjReverseSumsq>), dim3(grid), dim3(kProjThreads), 0, st, chunks,
+      DZ_LAUNCH((proj_kernel<DT, kProjReverseSumsq>), dim3(grid), dim3(kProjThreads), st, ev, chunks,
                          nchunks, ngroups, alpha, partials, counters);
       break;
     case kProjApplyF32:
-      hipLaunchKernelGGL((proj_kernel<DT, kProjApplyF32>), dim3(grid), dim3(kProjThreads), 0, st, chunks, nchunks,
+      DZ_LAUNCH((proj_kernel<DT, kProjApplyF32>), dim3(grid), dim3(kProjThreads), st, ev, chunks, nchunks,
                          ngroups, alpha, partials, counters);
       break;
     default:
@@ -1064,31 +1131,32 @@ static hipError_t launch_proj_dt(int mode, const DzChunk* chunks, uint32_t nchun
 }
 
 hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t ngroups,
-                       uint32_t grid, const void* alpha, double* partials, uint32_t* counters, hipStream_t st) {
+                       uint32_t grid, const void* alpha, double* partials, uint32_t* counters, hipStream_t st,
+                       const LaunchEvents& ev) {
   switch (dtype) {
     case DZ_F32:
-      return launch_proj_dt<DZ_F32>(mode, chunks, nchunks, ngroups, grid, alpha, partials, counters, st);
+      return launch_proj_dt<DZ_F32>(mode, chunks, nchunks, ngroups, grid, alpha, partials, counters, st, ev);
     case DZ_F16:
-      return launch_proj_dt<DZ_F16>(mode, chunks, nchunks, ngroups, grid, alpha, partials, counters, st);
+      return launch_proj_dt<DZ_F16>(mode, chunks, nchunks, ngroups, grid, alpha, partials, counters, st, ev);
     case DZ_BF16:
-      return launch_proj_dt<DZ_BF16>(mode, chunks, nchunks, ngroups, grid, alpha, partials, counters, st);
+      return launch_proj_dt<DZ_BF16>(mode, chunks, nchunks, ngroups, grid, alpha, partials, counters, st, ev);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_dot(int dtype, const DzChunk* chunks, uint32_t nchunks, const DzPtrArray& other,
-                      uint32_t group_base, double* partials, hipStream_t st) {
+                      uint32_t group_base, double* partials, hipStream_t st, const LaunchEvents& ev) {
   switch (dtype) {
     case DZ_F32:
-      hipLaunchKernelGGL((dot_kernel<DZ_F32>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other,
+      DZ_LAUNCH((dot_kernel<DZ_F32>), dim3(nchunks), dim3(kProjThreads), st, ev, chunks, other,
                          group_base, partials);
       break;
     case DZ_F16:
-      hipLaunchKernelGGL((dot_kernel<DZ_F16>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other,
+      DZ_LAUNCH((dot_kernel<DZ_F16>), dim3(nchunks), dim3(kProjThreads), st, ev, chunks, other,
                          group_base, partials);
       break;
     case DZ_BF16:
-      hipLaunchKernelGGL((dot_kernel<DZ_BF16>), dim3(nchunks), dim3(kProjThreads), 0, st, chunks, other,
+      DZ_LAUNCH((dot_kernel<DZ_BF16>), dim3(nchunks), dim3(kProjThreads), st, ev, chunks, other,
                          group_base, partials);
       break;
     default:
@@ -1098,18 +1166,19 @@ hipError_t launch_dot(int dtype, const DzChunk* chunks, uint32_t nchunks, const 
 }
 
 hipError_t launch_finalize(int dtype, const double* partials, const uint32_t* gbegin, uint32_t ngroups,
-                           double* sumsq, float* norm_f32, void* norm_T, bool take_sqrt, hipStream_t st) {
+                           double* sumsq, float* norm_f32, void* norm_T, bool take_sqrt, hipStream_t st,
+                           const LaunchEvents& ev) {
   switch (dtype) {
     case DZ_F32:
-      hipLaunchKernelGGL((finalize_kernel<DZ_F32>), dim3(ngroups), dim3(kProjThreads), 0, st,
+      DZ_LAUNCH((finalize_kernel<DZ_F32>), dim3(ngroups), dim3(kProjThreads), st, ev,
                          partials, gbegin, sumsq, norm_f32, norm_T, take_sqrt);
       break;
     case DZ_F16:
-      hipLaunchKernelGGL((finalize_kernel<DZ_F16>), dim3(ngroups), dim3(kProjThreads), 0, st,
+      DZ_LAUNCH((finalize_kernel<DZ_F16>), dim3(ngroups), dim3(kProjThreads), st, ev,
                          partials, gbegin, sumsq, norm_f32, norm_T, take_sqrt);
       break;
     case DZ_BF16:
-      hipLaunchKernelGGL((finalize_kernel<DZ_BF16>), dim3(ngroups), dim3(kProjThreads), 0, st,
+      DZ_LAUNCH((finalize_kernel<DZ_BF16>), dim3(ngroups), dim3(kProjThreads), st, ev,
                          partials, gbegin, sumsq, norm_f32, norm_T, take_sqrt);
       break;
     default:

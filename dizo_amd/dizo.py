@@ -185,7 +185,7 @@ class DiZO(nn.Module):
         if timer is None:
             fn()
         else:
-            with timer.span(name, passes * tab.bytes_per_tensor_pass):
+            with timer.span(name, passes * tab.bytes_per_tensor_pass, [tab]):
                 fn()
 
     def _group_norms(self, tab: ProjTable) -> torch.Tensor:

@@ -103,6 +103,16 @@ class _Table:
             raise DzError(f"{self.what}: a registered tensor's storage moved since the table was "
                           "built (rebuild the table)")
 
+    def time_next(self, start: "torch.cuda.Event | None", stop: "torch.cuda.Event | None") -> None:
+        """The next launching call on this table records `start` as its first
+        kernel starts and `stop` as its last kernel ends (either may be None).
+        The events must have been recorded once (so that they exist)."""
+        h = [None if e is None else e.cuda_event for e in (start, stop)]
+        if any(x == 0 for x in h):
+            raise DzError(f"{self.what}: timing events must be recorded once before time_next")
+        with torch.cuda.device(self.device):
+            L.call("dz_table_time_next", self.handle, h[0], h[1])
+
     def close(self) -> None:
         if getattr(self, "_h", None) is not None:
             h, self._h = self._h, None

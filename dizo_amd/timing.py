@@ -1,24 +1,32 @@
 """GPU-side timing of library launches with stream events.
 
-Each span records an event before and after its launches on the stream the
-launches go to (the caller's current stream), so the measured interval is
-the launches' device time when the stream is busy (back-to-back enqueue).
+A span times the launches made inside it with an event pair on the stream
+they go to (the caller's current stream). When the span is given the tables
+it launches through, the library records the pair itself as its first kernel
+starts and its last kernel ends (dz_table_time_next, hipExtLaunchKernel), so
+the interval is the kernels' device time even when the stream was idle and
+the host's launch work would otherwise fall inside it. Without tables, or
+while the stream is being captured into a graph, the span records the pair
+before and after its launches.
 """
 from __future__ import annotations
 
 from contextlib import contextmanager
-from typing import Dict, List, Tuple
+from typing import Dict, List, Sequence, Tuple
 
 import torch
 
 
 class KernelTimer:
-    def __init__(self, enabled: bool = True):
+    def __init__(self, enabled: bool = True, kernel_events: bool = True):
         self.enabled = enabled
+        self.kernel_events = kernel_events
         self.spans: Dict[str, List[Tuple[torch.cuda.Event, torch.cuda.Event, int]]] = {}
 
     @contextmanager
-    def span(self, name: str, nbytes: int = 0):
+    def span(self, name: str, nbytes: int = 0, tables: Sequence = ()):
+        """tables: the library tables the span's launches go through, in launch
+        order (each makes one launching call inside the span)."""
         if not self.enabled:
             yield
             return
@@ -26,10 +34,21 @@ class KernelTimer:
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
+        by_kernel = bool(tables) and self.kernel_events and not torch.cuda.is_current_stream_capturing()
+        if by_kernel:
+            # both events exist now (recorded once); the launches record them again
+            e1.record(stream)
+            first, last = tables[0], tables[-1]
+            if first is last:
+                first.time_next(e0, e1)
+            else:
+                first.time_next(e0, None)
+                last.time_next(None, e1)
         try:
             yield
         finally:
-            e1.record(stream)
+            if not by_kernel:
+                e1.record(stream)
             self.spans.setdefault(name, []).append((e0, e1, int(nbytes)))
 
     def reset(self) -> None:

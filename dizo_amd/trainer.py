@@ -387,7 +387,7 @@ class ZOTrainerMixin:
             for tab, _ in tabs.tables:
                 fn(tab)
         else:
-            with timer.span(what, tabs.bytes_per_pass):
+            with timer.span(what, tabs.bytes_per_pass, [tab for tab, _ in tabs.tables]):
                 for tab, _ in tabs.tables:
                     fn(tab)
 

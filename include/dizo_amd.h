@@ -81,6 +81,17 @@ int32_t dz_table_matches(const dz_table* t, const uint64_t* ptrs, int32_t n);
 /* Global z offset (element index of the tensor's first element) of tensor idx. */
 int32_t dz_table_z_offset(const dz_table* t, int32_t idx, uint64_t* out);
 
+/* Measurement hook; no counterpart in the reference (it serves the bench's
+ * per-pass timing). The next call on `t` that launches kernels (dz_perturb,
+ * dz_update, dz_restore_update, dz_restore_update_perturb, dz_group_sumsq,
+ * dz_project, dz_group_dot) records start_event when its first kernel starts
+ * and stop_event when its last kernel ends, through hipExtLaunchKernel, so
+ * the pair times the kernels without the host's launch work. Either may be
+ * NULL. Both are hipEvent_t handles the caller created (and has recorded at
+ * least once). The request is taken by that next call, whether or not it
+ * launches; do not set it on a stream being captured into a graph. */
+int32_t dz_table_time_next(dz_table* t, void* start_event, void* stop_event);
+
 /* ---- ZO step (trainer.py:1429-1444, 1570-1617) -------------------------- */
 /* Launches on one table share its work counters: order them on one stream
  * (never run two launches of the same table concurrently).

@@ -90,11 +90,14 @@ def _library_run(shape, dt, batches, steps, lr0, eps, seed=5, progress=_quiet, *
     return tr, losses, model, init
 
 
-def _reference_run(tr, init, dt, batches, steps, lr0, eps, norm, recipe=False, progress=_quiet):
+def _reference_run(tr, init, dt, batches, steps, lr0, eps, norm, recipe=False, progress=_quiet, ops=None):
     """The reference's expressions on a copy of the initial model, fed the z and
     gamma noise the library exports. recipe: the perturbation and update
     evaluated in the recipe form (exact products rounded as torch's CPU and
-    CUDA kernels round them) instead of by ROCm torch's fused kernels.
+    CUDA kernels round them) instead of by ROCm torch's fused kernels. ops: an
+    object with perturb / update methods of the same signatures, used instead
+    of either form (given the step index through ops.step; the run ends before
+    a step once ops.stop is set).
     Returns (losses, model, gamma)."""
     from dizo_amd import _lib as L
     from dizo_amd.synth import Cycle
@@ -111,11 +114,16 @@ def _reference_run(tr, init, dt, batches, steps, lr0, eps, norm, recipe=False, p
     dev = torch.device("cuda", 0)
     losses, gammas = [], None
     for k in range(steps):
+        if ops is not None and ops.stop:
+            break
         seed = np.random.randint(1000000000)
         zs = [tr.export_z(n, seed) for n in names]
         batch = batches[k % len(batches)]
         perturb = R.zo_perturb_parameters_recipe if recipe else R.zo_perturb_parameters
         update = R.zo_update_recipe if recipe else R.zo_update
+        if ops is not None:
+            ops.step = k
+            perturb, update = ops.perturb, ops.update
         perturb(params_b, zs, 1, eps)
         l1 = _ref_forward(model_b, batch)
         perturb(params_b, zs, -2, eps)
@@ -209,6 +217,88 @@ def test_c3_shape_200_step_loss_trajectory(capsys):
     same_c = int((_bits(torch.stack(la)) == _bits(torch.stack(lc))).sum())
     print(f"C3 vs recipe + torch.norm: {same_c}/200 losses bit-identical, max |dL| = {worst_c:.3g}", flush=True)
     assert worst_c <= 1e-3, f"max loss difference {worst_c} over 200 steps"
+    tr.zo_close()
+
+
+class _TieAudit:
+    """The recipe form of trainer.py:1438-1442 and 1603-1608 (what the library
+    computes), which at each of the reference's elementwise operations also
+    runs ROCm torch's own kernel on the same inputs and records where the two
+    differ. For every differing element it checks that the operation's fp32
+    result (the exact float64 value rounded to fp32, as torch's CPU and CUDA
+    kernels compute it) lies exactly halfway between the recipe's value and
+    ROCm torch's, i.e. that the two differ only in how an fp32 tie is rounded
+    to the parameter dtype."""
+
+    def __init__(self, names):
+        self.names = names
+        self.step = -1
+        self.stop = False      # set once a step has departed: the runs separate there
+        self.departures = []   # (step, op, tensor, numel, count)
+        self.non_ties = 0
+
+    def _check(self, rocm, exact64, op, i):
+        rec = exact64.float().to(rocm.dtype)
+        d = _bits(rec) != _bits(rocm)
+        n = int(d.sum())
+        if n:
+            x = exact64[d].float().double()
+            mid = (rec[d].double() + rocm[d].double()) * 0.5
+            self.non_ties += int((mid != x).sum())
+            self.departures.append((self.step, op, self.names[i], rocm.numel(), n))
+            self.stop = True
+        return rec
+
+    def perturb(self, params, zs, scaling_factor, zo_eps):
+        s, eps = R._f32(scaling_factor), R._f32(zo_eps)
+        assert scaling_factor in (1, -2)
+        for i, (param, z) in enumerate(zip(params, zs)):
+            a = scaling_factor * z   # exact: a product with 1 or -2 is never rounded
+            b = self._check(a * zo_eps, a.double() * eps, "(s*z)*eps", i)
+            param.data = self._check(param.data + b, param.data.double() + b.double(), "p+b", i)
+
+    def update(self, params, zs, projected_grad, lr):
+        g, lr32 = R._f32(projected_grad), R._f32(lr)
+        for i, (param, z) in enumerate(zip(params, zs)):
+            c = self._check(projected_grad * z, z.double() * g, "g*z", i)
+            d = self._check(lr * c, c.double() * lr32, "lr*(g*z)", i)
+            param.data = self._check(param.data - d, param.data.double() - d.double(), "p-d", i)
+
+
+def test_c3_rocm_torch_departs_from_the_recipe_only_on_fp32_ties(capsys):
+    """Why ROCm torch's own kernels separate from the library at C3's shape.
+
+    Along the library's 200-step C3 trajectory (the recipe form, bit-exact with
+    the library by test_c3_shape_200_step_loss_trajectory), every elementwise
+    operation of the reference's perturbation and update is also run by ROCm
+    torch's kernel on the same tensors, up to the end of the first step where
+    the two differ. Before that step the ROCm torch run is the same run, so its
+    differing elements are where that run leaves the recipe. At every one of
+    them the fp32 result of the operation is exactly halfway between the two
+    values: ROCm torch rounded an fp32 tie to the other neighbour (it rounds
+    the exact product once on its non-vectorised launch paths, asserted on
+    constructed ties in tests/test_gpu_zo.py)."""
+    from dizo_amd.synth import make_batches
+    from dizo_amd.trainer import select_trainable
+    batches = make_batches(8, 16, 50272, seed=82, device="cuda", min_len=32, max_len=64)
+    report = _reporter(capsys)
+    tr, la, ma, init = _library_run("opt-2.7b", torch.float16, batches, 200, 1e-6, 1e-3, progress=report)
+    del ma
+    torch.cuda.empty_cache()
+    audit = _TieAudit([n for n, _ in select_trainable(init)[0]])
+    lb, mb, gb = _reference_run(tr, init, torch.float16, batches, 200, 1e-6, 1e-3, _lib_norm, ops=audit,
+                                progress=report)
+    bad = [k for k, (a, b) in enumerate(zip(la, lb)) if not _same(a, b)]
+    assert not bad, f"the audited recipe left the library's trajectory at steps {bad[:5]}"
+    deps = audit.departures
+    assert deps, "ROCm torch's kernels matched the recipe at every operation of the 200 steps"
+    total = sum(d[4] for d in deps)
+    print(f"ROCm torch vs recipe at C3: first departure at step {deps[0][0]} ({len(lb)} steps audited): "
+          f"{total} elements in {len(deps)} tensor ops differ, {audit.non_ties} of them not fp32 ties",
+          flush=True)
+    for d in deps[:8]:
+        print(f"  step {d[0]} {d[1]} {d[2]} ({d[3]} elements): {d[4]}", flush=True)
+    assert audit.non_ties == 0
     tr.zo_close()
 
 
