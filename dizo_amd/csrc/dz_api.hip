@@ -210,6 +210,7 @@ static __device__ __align__(256) unsigned char scratch[kStaticBytes];
 struct ChunkList {
   uint32_t elems = 0;  // tile size (elements)
   uint32_t n = 0;      // number of tiles
+  uint32_t nfull = 0;  // the first nfull tiles are full and aligned
   DzChunk* d = nullptr;
 };
 
@@ -220,6 +221,7 @@ struct dz_table {
   int32_t n = 0;
   uint32_t chunk_elems = 0;  // tile size of the primary list (d_chunks)
   uint32_t nchunks = 0;
+  uint32_t nfull = 0;        // ZO tables: the primary list's full, aligned tiles come first
   std::vector<uint64_t> ptrs, aux, zoff;
   std::vector<int64_t> numels;
   std::vector<uint32_t> group_begin;  // n + 1 chunk indices (primary list)
@@ -296,14 +298,15 @@ int32_t rmw(dz_table* t, int mode, const dz::DzScalars& s, const dz::DzScalarPtr
   if (t->projection) return fail(DZ_ERR_INVALID, "perturb/update need a ZO table (created without anchors)");
   const uint32_t want = (uint32_t)dz::rmw_chunk_elems(t->dtype, mode);
   const DzChunk* chunks = t->d_chunks;
-  uint32_t ntiles = t->nchunks;
+  uint32_t ntiles = t->nchunks, nfull = t->nfull;
   if (want != t->chunk_elems) {
     if (want != t->extra.elems) return fail(DZ_ERR_INVALID, "internal: no tile list for this launch");
     chunks = t->extra.d;
     ntiles = t->extra.n;
+    nfull = t->extra.nfull;
   }
   if (ntiles == 0) return DZ_OK;
-  hipError_t e = dz::launch_rmw(t->dtype, mode, chunks, ntiles, rmw_grid(t, mode, ntiles),
+  hipError_t e = dz::launch_rmw(t->dtype, mode, chunks, ntiles, nfull, rmw_grid(t, mode, ntiles),
                                 t->dev->tab[t->dtype], s, p, t->d_counters, (hipStream_t)stream, ev);
   if (e != hipSuccess) return hip_fail(e, "rmw kernel launch");
   return DZ_OK;
@@ -330,6 +333,17 @@ void build_chunks(const dz_table* t, uint32_t elems, std::vector<DzChunk>* out,
     }
     if (group_begin) group_begin->push_back((uint32_t)out->size());
   }
+}
+
+// ZO tile lists: full, aligned tiles first (in tensor order), then the
+// partial or misaligned ones; returns the number of full tiles. The order of
+// the tiles changes no result (z is a function of the element index), and it
+// lets the RMW kernel run its full tiles without a per-tile shape test.
+uint32_t full_tiles_first(std::vector<DzChunk>* v, uint32_t elems) {
+  auto it = std::stable_partition(v->begin(), v->end(), [elems](const DzChunk& c) {
+    return c.n == elems && (c.meta & kDzMetaAligned) != 0u;
+  });
+  return (uint32_t)(it - v->begin());
 }
 
 // Rejects a table in which a range the kernels write (theta) overlaps another
@@ -509,8 +523,9 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
     return rc;
   }
   std::vector<DzChunk> chunks;
-  build_chunks(t, t->chunk_elems, &chunks, &t->group_begin);
+  build_chunks(t, t->chunk_elems, &chunks, t->projection ? &t->group_begin : nullptr);
   t->nchunks = (uint32_t)chunks.size();
+  if (!t->projection) t->nfull = full_tiles_first(&chunks, t->chunk_elems);
   hipError_t e = upload_chunks(chunks, &t->d_chunks);
   if (e == hipSuccess && !t->projection) {
     const uint32_t narrow = (uint32_t)dz::rmw_chunk_elems(dtype, dz::kModePerturb);
@@ -519,6 +534,7 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
       build_chunks(t, narrow, &fine, nullptr);
       t->extra.elems = narrow;
       t->extra.n = (uint32_t)fine.size();
+      t->extra.nfull = full_tiles_first(&fine, narrow);
       e = upload_chunks(fine, &t->extra.d);
     }
   }

@@ -73,14 +73,29 @@ __host__ __device__ constexpr int rmw_lds_table_bytes(int dtype, int mode) {
   return (dtype == DZ_F32 || rmw_pair_mode(mode)) ? kDzTabEntries * 4 : kDzTabEntries * 2;
 }
 
-// Work counters of a table, one set per table: kCounters tile dispensers 128
-// bytes apart, then the number of finished workgroups. Zeroed when the table
-// is created; the last workgroup of every RMW launch puts them back to zero,
-// so consecutive launches on one stream need no reset (and no memset in a
-// captured graph). Launches of one table must not overlap in time.
+// Work counters of a table, one set per table, 128 bytes apart: kCounters
+// tile dispensers for workgroup-level loops, kSliceCounters slice
+// dispensers for the RMW kernel's wave-level loop (it hands out 16 times as
+// many work items), then (slot kDoneSlot) the number of finished
+// workgroups. Zeroed when the table is created; the last workgroup of every
+// launch puts them back to zero, so consecutive launches on one stream need
+// no reset (and no memset in a captured graph). Launches of one table must
+// not overlap in time.
+// RMW launches that run the wave-level loop: bit 4 * dtype + mode (dtype
+// DZ_F32 0, DZ_F16 1, DZ_BF16 2; mode as RmwMode); the others run the
+// workgroup-level loop. Measured on the MI355X: the wave-level loop is
+// faster only for the bf16 restore+update+next perturb pass (OPT-30B: 22.9
+// against 24.0 ms), whose ALU work per tile is the largest; every streaming
+// pass runs slower with it (OPT-13B fp16 perturb 7.92 against 7.71 ms,
+// OPT-125m fp32 0.149 against 0.125 ms).
+#ifndef DZ_RMW_SLICE_MASK
+#define DZ_RMW_SLICE_MASK (1 << (4 * 2 + 3))
+#endif
 constexpr int kCounters = DZ_RMW_COUNTERS;
+constexpr int kSliceCounters = 16;
+constexpr int kDoneSlot = kCounters > kSliceCounters ? kCounters : kSliceCounters;
 constexpr int kCounterStride = 32;  // uint32 slots (128 bytes)
-constexpr int kCounterWords = (kCounters + 1) * kCounterStride;
+constexpr int kCounterWords = (kDoneSlot + 1) * kCounterStride;
 
 // Projection kernel geometry: persistent 1024-thread workgroups, DZ_PROJ_WG_PER_CU
 // per CU, taking 32768-element chunks (64 KB of theta and 64 KB of theta0 in
@@ -127,7 +142,9 @@ struct LaunchEvents {
   hipEvent_t stop = nullptr;
 };
 
-hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
+// The first nfull chunks are full, aligned tiles; the rest are partial or
+// misaligned.
+hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t nfull, uint32_t grid,
                       const void* qtab, const DzScalars& s, const DzScalarPtrs& p, uint32_t* counters,
                       hipStream_t st, const LaunchEvents& ev = {});
 // Persistent: `grid` workgroups share the chunks through `counters` (zero

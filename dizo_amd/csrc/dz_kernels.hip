@@ -137,6 +137,7 @@ struct RmwTraits {
   // Waves per SIMD: 4 with one workgroup per CU (128 VGPRs per lane), 8 when
   // two workgroups share a CU (64 VGPRs).
   static constexpr int kWavesPerEU = (kWide || DZ_RMW_NARROW_WG_PER_CU == 1) ? 4 : 8;
+  static constexpr bool kSlices = ((DZ_RMW_SLICE_MASK >> (4 * DT + MODE)) & 1) != 0;
 };
 
 // Table entry for z = +Q_T[i] (qbits = bits of Q_T[i]).
@@ -223,6 +224,16 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 // R_bf16(a + b) lane by lane for packed bf16 words, the fp32 sums written out.
 __device__ __forceinline__ uint32_t add_pair_bf16(uint32_t a, uint32_t b) {
   return pack_bf16(bf16_lo_f(a) + bf16_lo_f(b), bf16_hi_f(a) + bf16_hi_f(b));
+}
+// R_bf16(x) as an fp32 value: v_cvt_pk_bf16_f32 with a zero low lane leaves
+// the rounded bf16 in the high half and zeros below it, which is the fp32
+// bit pattern of the rounded value (no unpacking before the next fp32 add).
+// Written as the instruction: from pack_bf16(0.0f, x) the compiler converts
+// into the low lane and moves the result up with a v_perm_b32.
+__device__ __forceinline__ float round_bf16_f(float x) {
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
+  return __uint_as_float(r);
 }
 
 // R_T(a + b) for a pair of 16-bit values packed in one word: fp16 adds
@@ -337,20 +348,34 @@ __device__ __forceinline__ uint32_t combine_pair16(uint32_t th, uint32_t w, uint
     }
     return r;
   }
-  const uint32_t sw = w & 0x80008000u;
   if constexpr (!rmw_pair_mode(MODE)) {
-    return add_pair<DT>(th, (t.e0 | (t.e1 << 16)) ^ sw);
+    return add_pair<DT>(th, (t.e0 | (t.e1 << 16)) ^ (w & 0x80008000u));
   } else {
-    // entry = b | (-d) << 16 for a positive z (bf16 here: the fp16 pair modes
-    // return above)
-    const uint32_t b = pack_lo(t.e0, t.e1) ^ sw;
-    const uint32_t nd = pack_hi(t.e0, t.e1) ^ sw;
-    uint32_t r = add_pair<DT>(add_pair<DT>(th, b), nd);
+    // bf16 (the fp16 pair modes return above). entry = b | (-d) << 16 for a
+    // positive z. Each signed table value is taken straight to its fp32 bit
+    // pattern: the low-half value of element 0 as (e0 + s0) << 16 with s0 its
+    // sign at bit 15 (adding 0x8000 below bit 16 flips bit 15 whatever the
+    // carry), a high-half value as (e & 0xffff0000) ^ sign at bit 31, the
+    // low-half value of element 1 as (e1 << 16) + sign at bit 31. The three
+    // adds are the reference's fp32 adds, each rounded to bf16 (round_bf16_f
+    // for the first two, one packing conversion for the last).
+    const uint32_t s0 = w & 0x8000u, s0h = s0 << 16, s1 = w & 0x80000000u;
+    const float b0 = __uint_as_float((t.e0 + s0) << 16);
+    const float b1 = __uint_as_float((t.e1 << 16) + s1);
+    const float nd0 = __uint_as_float((t.e0 & 0xffff0000u) ^ s0h);
+    const float nd1 = __uint_as_float((t.e1 & 0xffff0000u) ^ s1);
+    float lo = round_bf16_f(bf16_lo_f(th) + b0);
+    float hi = round_bf16_f(bf16_hi_f(th) + b1);
     if constexpr (MODE == kModeRestoreUpdatePerturb) {
+      lo = round_bf16_f(lo + nd0);
+      hi = round_bf16_f(hi + nd1);
       // the next step's +1 perturbation uses the same b (same scale and eps)
-      r = add_pair<DT>(r, pack_lo(t.f0, t.f1) ^ (w2 & 0x80008000u));
+      const float c0 = __uint_as_float((t.f0 + (w2 & 0x8000u)) << 16);
+      const float c1 = __uint_as_float((t.f1 << 16) + (w2 & 0x80000000u));
+      return pack_bf16(lo + c0, hi + c1);
+    } else {
+      return pack_bf16(lo + nd0, hi + nd1);
     }
-    return r;
   }
 }
 
@@ -444,46 +469,52 @@ __device__ __forceinline__ bool full_tile(const DzChunk& ch) {
   return ch.n == (uint32_t)RmwTraits<DT, MODE>::kChunk && (ch.meta & kDzMetaAligned) != 0u;
 }
 
-// Byte offset of vector i of this thread in a full tile: group u = i (16-bit)
-// or i / 2 (fp32, two vectors per group of 8 elements); groups are strided
-// by the workgroup so each load instruction covers contiguous memory.
-template <int DT>
-__device__ __forceinline__ size_t tile_vec_offset(int i) {
+// Lane layouts of a full tile. A thread's groups of 8 elements are g0 + u *
+// kStride for u < G (chunk-local group indices), so each load instruction of
+// the kStride threads that share a layout covers contiguous memory:
+//   workgroup layout: kStride = 1024, g0 = threadIdx.x (the workgroup takes
+//                     the whole tile);
+//   slice layout:     kStride = 64, g0 = first + lane (a wave takes the 64 * G
+//                     groups of one slice of the tile, starting at `first`).
+// Byte offset of vector i: group u = i (16-bit) or i / 2 (fp32, two vectors
+// per group).
+template <int DT, int kStride>
+__device__ __forceinline__ size_t tile_vec_offset(uint32_t g0, int i) {
   if constexpr (DT != DZ_F32) {
-    return (size_t)(threadIdx.x + i * kRmwThreads) * 16;
+    return (size_t)(g0 + (uint32_t)i * kStride) * 16;
   } else {
-    return (size_t)(threadIdx.x + (i >> 1) * kRmwThreads) * 32 + (size_t)(i & 1) * 16;
+    return (size_t)(g0 + (uint32_t)(i >> 1) * kStride) * 32 + (size_t)(i & 1) * 16;
   }
 }
 
-template <int DT, int MODE>
-__device__ __forceinline__ void load_tile(const DzChunk& ch, TileRegs<DT, MODE>& r) {
-  const char* base = (const char*)ch.ptr;
+template <int DT, int MODE, int kStride>
+__device__ __forceinline__ void load_tile_at(uint64_t addr, uint32_t g0, TileRegs<DT, MODE>& r) {
+  const char* base = (const char*)addr;
 #pragma unroll
-  for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_stream(base + tile_vec_offset<DT>(i));
+  for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_stream(base + tile_vec_offset<DT, kStride>(g0, i));
 }
 
-// Philox block of group u of a full tile: counter zgroup + threadIdx.x +
-// u * kRmwThreads. kUniformHi: the counters' high words agree across the tile
-// (its low word does not wrap), so the high word is wave-uniform and round 0's
-// xor and round 1's first product run on the scalar unit, one v_mad_u64_u32
-// less per block.
-template <bool kUniformHi>
-__device__ __forceinline__ DzU4 tile_block(const DzChunk& ch, uint64_t seed, int u) {
+// Philox block of group g0 + u * kStride: counter zgroup + that group.
+// kUniformHi: the counters' high words agree across the span of groups the
+// layout covers (the low word does not wrap there), so the high word is
+// wave-uniform and round 0's xor and round 1's first product run on the
+// scalar unit, one v_mad_u64_u32 less per block.
+template <bool kUniformHi, int kStride>
+__device__ __forceinline__ DzU4 tile_block(const DzChunk& ch, uint64_t seed, uint32_t g0, int u) {
   if constexpr (kUniformHi) {
-    const uint32_t lo = (uint32_t)ch.zgroup + threadIdx.x + u * kRmwThreads;
+    const uint32_t lo = (uint32_t)ch.zgroup + g0 + (uint32_t)u * kStride;
     return dz_philox_counter(seed, kDzStreamParam, lo, (uint32_t)(ch.zgroup >> 32));
   } else {
-    return dz_philox_group(seed, kDzStreamParam, ch.zgroup + threadIdx.x + u * kRmwThreads);
+    return dz_philox_group(seed, kDzStreamParam, ch.zgroup + g0 + (uint32_t)u * kStride);
   }
 }
 
 // Group u of a full fp32 tile with its z words w (and next-step words w2):
 // the launch's operation applied and the group stored.
-template <int DT, int MODE>
-__device__ __forceinline__ void apply_store_group32(char* base, const TileRegs<DT, MODE>& r, int u, const DzU4& w,
-                                                    const DzU4& w2, const typename RmwTraits<DT, MODE>::E* tab,
-                                                    const DzScalars& sc) {
+template <int DT, int MODE, int kStride>
+__device__ __forceinline__ void apply_store_group32(char* base, uint32_t g0, const TileRegs<DT, MODE>& r, int u,
+                                                    const DzU4& w, const DzU4& w2,
+                                                    const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc) {
   const dz_u32x4 a = r.v[2 * u], b = r.v[2 * u + 1];
   dz_u32x4 o0, o1;
   o0.x = apply_one<DT, MODE>(a.x, w.x & 0xffffu, w2.x & 0xffffu, tab, sc);
@@ -494,18 +525,19 @@ __device__ __forceinline__ void apply_store_group32(char* base, const TileRegs<D
   o1.y = apply_one<DT, MODE>(b.y, w.z >> 16, w2.z >> 16, tab, sc);
   o1.z = apply_one<DT, MODE>(b.z, w.w & 0xffffu, w2.w & 0xffffu, tab, sc);
   o1.w = apply_one<DT, MODE>(b.w, w.w >> 16, w2.w >> 16, tab, sc);
-  st_stream(base + tile_vec_offset<DT>(2 * u), o0);
-  st_stream(base + tile_vec_offset<DT>(2 * u + 1), o1);
+  st_stream(base + tile_vec_offset<DT, kStride>(g0, 2 * u), o0);
+  st_stream(base + tile_vec_offset<DT, kStride>(g0, 2 * u + 1), o1);
 }
 
-// A full tile as one straight-line block: the Philox blocks of all its
-// groups, then the lookups, adds and stores. Keeping both in one basic block
-// (the branch on the counters' high word is taken once per tile, outside it)
-// lets the scheduler overlap the ALU work of the Philox chains with the LDS
-// lookups; with the chains in a block of their own the two ran one after the
-// other (three-way pass at OPT-13B: 8.9 -> 8.2 ms at equal Philox rounds).
-template <int DT, int MODE, bool kUniformHi>
-__device__ __forceinline__ void tile_body(const DzChunk& ch, const TileRegs<DT, MODE>& r,
+// A thread's share of a full tile as one straight-line block: the Philox
+// blocks of all its groups, then the lookups, adds and stores. Keeping both
+// in one basic block (the branch on the counters' high word is taken once
+// per tile, outside it) lets the scheduler overlap the ALU work of the Philox
+// chains with the LDS lookups; with the chains in a block of their own the
+// two ran one after the other (three-way pass at OPT-13B: 8.9 -> 8.2 ms at
+// equal Philox rounds).
+template <int DT, int MODE, bool kUniformHi, int kStride>
+__device__ __forceinline__ void tile_body(const DzChunk& ch, uint32_t g0, const TileRegs<DT, MODE>& r,
                                           const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc) {
   constexpr int G = RmwTraits<DT, MODE>::kGroups;
   constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
@@ -513,45 +545,50 @@ __device__ __forceinline__ void tile_body(const DzChunk& ch, const TileRegs<DT, 
   DzU4 w[G], w2[G];
 #pragma unroll
   for (int u = 0; u < G; ++u) {
-    w[u] = tile_block<kUniformHi>(ch, sc.seed, u);
-    w2[u] = kTwoSeeds ? tile_block<kUniformHi>(ch, sc.seed2, u) : w[u];
+    w[u] = tile_block<kUniformHi, kStride>(ch, sc.seed, g0, u);
+    w2[u] = kTwoSeeds ? tile_block<kUniformHi, kStride>(ch, sc.seed2, g0, u) : w[u];
   }
 #pragma unroll
   for (int u = 0; u < G; ++u) {
     if constexpr (DT == DZ_F32) {
-      apply_store_group32<DT, MODE>(base, r, u, w[u], w2[u], tab, sc);
+      apply_store_group32<DT, MODE, kStride>(base, g0, r, u, w[u], w2[u], tab, sc);
     } else {
       dz_u32x4 o;
       o.x = combine_pair16<DT, MODE>(r.v[u].x, w[u].x, w2[u].x, lookup_pair16<DT, MODE>(w[u].x, w2[u].x, tab));
       o.y = combine_pair16<DT, MODE>(r.v[u].y, w[u].y, w2[u].y, lookup_pair16<DT, MODE>(w[u].y, w2[u].y, tab));
       o.z = combine_pair16<DT, MODE>(r.v[u].z, w[u].z, w2[u].z, lookup_pair16<DT, MODE>(w[u].z, w2[u].z, tab));
       o.w = combine_pair16<DT, MODE>(r.v[u].w, w[u].w, w2[u].w, lookup_pair16<DT, MODE>(w[u].w, w2[u].w, tab));
-      st_stream(base + tile_vec_offset<DT>(u), o);
+      st_stream(base + tile_vec_offset<DT, kStride>(g0, u), o);
     }
   }
 }
 
-// Applies the launch's operation to a full tile already in registers and stores it.
-template <int DT, int MODE>
-__device__ __forceinline__ void compute_store_tile(const DzChunk& ch, const TileRegs<DT, MODE>& r,
+// Applies the launch's operation to a thread's share of a full tile, already
+// in registers, and stores it. The layout covers groups first .. first +
+// G * kStride - 1 of the tile.
+template <int DT, int MODE, int kStride>
+__device__ __forceinline__ void compute_store_tile(const DzChunk& ch, uint32_t g0, uint32_t first,
+                                                   const TileRegs<DT, MODE>& r,
                                                    const typename RmwTraits<DT, MODE>::E* tab,
                                                    const DzScalars& sc) {
   constexpr int G = RmwTraits<DT, MODE>::kGroups;
-  if ((uint32_t)ch.zgroup <= 0xffffffffu - (uint32_t)(G * kRmwThreads - 1)) {
-    tile_body<DT, MODE, true>(ch, r, tab, sc);
+  if ((uint32_t)ch.zgroup + first <= 0xffffffffu - (uint32_t)(G * kStride - 1) &&
+      (uint32_t)ch.zgroup + first >= (uint32_t)ch.zgroup) {
+    tile_body<DT, MODE, true, kStride>(ch, g0, r, tab, sc);
   } else {
-    tile_body<DT, MODE, false>(ch, r, tab, sc);
+    tile_body<DT, MODE, false, kStride>(ch, g0, r, tab, sc);
   }
 }
 
-// Partial or misaligned tile: element by element, bounds-checked.
-template <int DT, int MODE>
-__device__ __forceinline__ void rmw_partial(const DzChunk& ch, const typename RmwTraits<DT, MODE>::E* tab,
-                                            const DzScalars& sc) {
+// Partial or misaligned tile, element by element and bounds-checked: groups
+// first + lane, first + lane + kStride, ... below `end` (and inside the tile).
+template <int DT, int MODE, int kStride>
+__device__ __forceinline__ void rmw_partial(const DzChunk& ch, uint32_t first, uint32_t end, uint32_t lane,
+                                            const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc) {
   using S = typename DT_<DT>::S;
   constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
   char* base = (char*)ch.ptr;
-  for (uint32_t g = threadIdx.x; g * 8u < ch.n; g += kRmwThreads) {
+  for (uint32_t g = first + lane; g < end && g * 8u < ch.n; g += kStride) {
     const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
     const DzU4 w2 = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, ch.zgroup + g) : w;
     const uint32_t m = min(8u, ch.n - g * 8u);
@@ -566,62 +603,65 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, const typename Rm
 
 // ---------------------------------------------------------------------------
 // Multi-tensor read-modify-write kernel (perturb / update / restore+update).
-// Persistent workgroups build the launch's delta table in LDS, then take
-// tiles from the table's work counters (counter j of the K in use hands out
-// tiles j, j + K, j + 2K, ...; workgroup b uses counter (b / 8) mod K, so each
-// counter serves workgroups on every XCD, and K = min(8, grid / 8) so each
-// counter has workgroups). Handing out tiles dynamically keeps the tiles in
-// flight close together in memory and lets fast workgroups take more tiles,
-// which a static grid-stride split does not; the next tile index is fetched
-// while the current tile is processed. The last workgroup to finish resets
-// the counters for the next launch.
+// Persistent workgroups (one per CU) build the launch's delta table in LDS,
+// then take work from the table's counters, handed out dynamically: that
+// keeps the work in flight close together in memory and lets fast
+// workgroups take more, which a static grid-stride split does not. The
+// chunk list holds its nfull full, aligned tiles first. The last workgroup to
+// finish resets the counters for the next launch.
+//
+// Wave-level loop (RmwTraits::kSlices): each wave takes slices of 64 * G
+// groups (a sixteenth of a tile; slice id = ticket * K + j from counter j of
+// the K = 16 in use, wave w of workgroup b using counter ((b / 8) * 16 + w)
+// mod K, so every counter serves waves on every XCD) and loads, computes and
+// stores them on its own, with no barrier between slices: while one wave
+// waits for memory, the other waves of its SIMD compute. With a barrier per
+// tile, all 16 waves of a workgroup load, wait, compute and store in step,
+// and a tile's load latency and its compute add up instead of overlapping.
+//
+// Workgroup-level loop (the other launches): the workgroup takes whole
+// tiles from counters j of K = min(8, grid / 8), workgroup b using counter
+// (b / 8) mod K; wave 0 keeps a ring in LDS (while tile k streams, the index
+// of tile k+3 is taken and the descriptor of tile k+2 is loaded) and a
+// barrier ends each tile.
 // ---------------------------------------------------------------------------
 template <int DT, int MODE>
-__global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU)) rmw_kernel(const DzChunk* __restrict__ chunks,
-                                                          uint32_t nchunks,
-                                                          const void* __restrict__ qtab,
-                                                          DzScalars sc_in, DzScalarPtrs sp,
-                                                          uint32_t* __restrict__ counters) {
-  using Tr = RmwTraits<DT, MODE>;
-  using E = typename Tr::E;
-  __shared__ __attribute__((aligned(16))) E tab[kDzTabEntries];
-  // Tile bookkeeping rings: indices of tiles k .. k+3, descriptors of k .. k+2.
-  __shared__ uint32_t sidx[4];
-  __shared__ DzChunk sdesc[3];
-  const DzScalars sc = resolve_scalars<DT>(sc_in, sp);
-  // Counters in use: every one of them must be served by at least one
-  // workgroup, or its tiles would never be taken (a small grid uses fewer).
-  const uint32_t ncnt = rfl_u32(max(1u, min((uint32_t)kCounters, gridDim.x >> 3)));
-  const uint32_t j = rfl_u32((blockIdx.x >> 3) % ncnt);
+__device__ __forceinline__ void rmw_slices(const DzChunk* __restrict__ chunks, uint32_t nchunks, uint32_t nfull,
+                                           const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
+                                           uint32_t* __restrict__ counters) {
+  constexpr uint32_t G = RmwTraits<DT, MODE>::kGroups;
+  constexpr uint32_t kSlices = kRmwThreads / 64;  // slices per tile
+  constexpr uint32_t ncnt = (uint32_t)kSliceCounters;
+  static_assert(kSliceCounters <= kRmwThreads / 64, "every slice counter needs a wave of workgroup 0");
+  const uint32_t wave = rfl_u32(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t j = rfl_u32(((blockIdx.x >> 3) * kSlices + wave) % ncnt);
   uint32_t* mine = counters + j * kCounterStride;
-  const uint64_t nch = nchunks;
-  // Pipeline kept by wave 0: while tile k streams, the index of tile k+3 is
-  // taken from the counter and the descriptor of tile k+2 is loaded, so
-  // neither latency sits between two tiles. A tile's data is loaded when its
-  // turn comes: loading tile k + 1 during tile k measured slower for every
-  // mode (16-bit at OPT-13B, fp32 at OPT-125m). Start-up: lane 0 takes the
-  // first three tickets with one atomic, the table's loads are issued behind
-  // it, then the first two descriptors are loaded (clamped to a valid index;
-  // only tickets below nchunks are used) and the table is written.
-  uint32_t t0 = 0;
-  if (threadIdx.x == 0) t0 = atomicAdd(mine, 3u);
-  TableSlices<DT> qs;
-  load_table<DT>(qs, qtab);
-  if (threadIdx.x == 0) {
-    uint64_t c[3];
-    for (int i = 0; i < 3; ++i) {
-      c[i] = (uint64_t)(t0 + i) * ncnt + j;
-      sidx[i] = (uint32_t)min(c[i], nch);
-    }
-    if (nch > 0) {
-      const DzChunk d0 = chunks[min(c[0], nch - 1)];
-      const DzChunk d1 = chunks[min(c[1], nch - 1)];
-      sdesc[0] = d0;
-      sdesc[1] = d1;
+  const uint64_t nslices = (uint64_t)nchunks * kSlices;
+  TileRegs<DT, MODE> r;
+  for (;;) {
+    uint32_t t = 0;
+    if (lane == 0) t = atomicAdd(mine, 1u);
+    const uint64_t sid = (uint64_t)rfl_u32(t) * ncnt + j;  // lane 0 is the first active lane
+    if (sid >= nslices) break;
+    const uint32_t c = (uint32_t)(sid / kSlices);
+    const uint32_t first = (uint32_t)(sid % kSlices) * 64u * G;
+    const DzChunk ch = uniform_chunk(chunks[c]);
+    if (c < nfull) {
+      load_tile_at<DT, MODE, 64>(ch.ptr, first + lane, r);
+      compute_store_tile<DT, MODE, 64>(ch, first + lane, first, r, tab, sc);
+    } else {
+      rmw_partial<DT, MODE, 64>(ch, first, first + 64u * G, lane, tab, sc);
     }
   }
-  store_table<DT, MODE>(tab, qs, sc);
-  __syncthreads();
+}
+
+template <int DT, int MODE>
+__device__ __forceinline__ void rmw_tiles(const DzChunk* __restrict__ chunks, uint32_t nchunks,
+                                          const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
+                                          uint32_t* sidx, DzChunk* sdesc, uint32_t* mine, uint32_t ncnt,
+                                          uint32_t j) {
+  const uint64_t nch = nchunks;
   TileRegs<DT, MODE> cur;
   for (uint32_t k = 0;; ++k) {
     const uint32_t c = sidx[k % 4];
@@ -647,10 +687,10 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
       }
     }
     if (full_tile<DT, MODE>(ch)) {
-      load_tile<DT, MODE>(ch, cur);
-      compute_store_tile<DT, MODE>(ch, cur, tab, sc);
+      load_tile_at<DT, MODE, kRmwThreads>(ch.ptr, threadIdx.x, cur);
+      compute_store_tile<DT, MODE, kRmwThreads>(ch, threadIdx.x, 0u, cur, tab, sc);
     } else {
-      rmw_partial<DT, MODE>(ch, tab, sc);
+      rmw_partial<DT, MODE, kRmwThreads>(ch, 0u, 0xffffffffu, threadIdx.x, tab, sc);
     }
     if (threadIdx.x == 0) {
       sidx[(k + 3) % 4] = (uint32_t)min((uint64_t)grabbed * ncnt + j, nch);
@@ -665,10 +705,64 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
     }
     __syncthreads();
   }
+}
+
+template <int DT, int MODE>
+__global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU)) rmw_kernel(const DzChunk* __restrict__ chunks,
+                                                          uint32_t nchunks, uint32_t nfull,
+                                                          const void* __restrict__ qtab,
+                                                          DzScalars sc_in, DzScalarPtrs sp,
+                                                          uint32_t* __restrict__ counters) {
+  using Tr = RmwTraits<DT, MODE>;
+  using E = typename Tr::E;
+  __shared__ __attribute__((aligned(16))) E tab[kDzTabEntries];
+  const DzScalars sc = resolve_scalars<DT>(sc_in, sp);
+  if constexpr (Tr::kSlices) {
+    TableSlices<DT> qs;
+    load_table<DT>(qs, qtab);
+    store_table<DT, MODE>(tab, qs, sc);
+    __syncthreads();
+    rmw_slices<DT, MODE>(chunks, nchunks, nfull, tab, sc, counters);
+    __syncthreads();  // every wave of the workgroup has taken its last ticket
+  } else {
+    // Tile bookkeeping rings: indices of tiles k .. k+3, descriptors of k .. k+2.
+    __shared__ uint32_t sidx[4];
+    __shared__ DzChunk sdesc[3];
+    // Counters in use: every one of them must be served by at least one
+    // workgroup, or its tiles would never be taken (a small grid uses fewer).
+    const uint32_t ncnt = rfl_u32(max(1u, min((uint32_t)kCounters, gridDim.x >> 3)));
+    const uint32_t j = rfl_u32((blockIdx.x >> 3) % ncnt);
+    uint32_t* mine = counters + j * kCounterStride;
+    const uint64_t nch = nchunks;
+    // Start-up: lane 0 takes the first three tickets with one atomic, the
+    // table's loads are issued behind it, then the first two descriptors are
+    // loaded (clamped to a valid index; only tickets below nchunks are used)
+    // and the table is written.
+    uint32_t t0 = 0;
+    if (threadIdx.x == 0) t0 = atomicAdd(mine, 3u);
+    TableSlices<DT> qs;
+    load_table<DT>(qs, qtab);
+    if (threadIdx.x == 0) {
+      uint64_t c[3];
+      for (int i = 0; i < 3; ++i) {
+        c[i] = (uint64_t)(t0 + i) * ncnt + j;
+        sidx[i] = (uint32_t)min(c[i], nch);
+      }
+      if (nch > 0) {
+        const DzChunk d0 = chunks[min(c[0], nch - 1)];
+        const DzChunk d1 = chunks[min(c[1], nch - 1)];
+        sdesc[0] = d0;
+        sdesc[1] = d1;
+      }
+    }
+    store_table<DT, MODE>(tab, qs, sc);
+    __syncthreads();
+    rmw_tiles<DT, MODE>(chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j);
+  }
   if (threadIdx.x == 0) {
-    const uint32_t done = atomicAdd(counters + kCounters * kCounterStride, 1u);
+    const uint32_t done = atomicAdd(counters + kDoneSlot * kCounterStride, 1u);
     if (done == gridDim.x - 1) {
-      for (int i = 0; i <= kCounters; ++i) atomicExch(counters + i * kCounterStride, 0u);
+      for (int i = 0; i <= kDoneSlot; ++i) atomicExch(counters + i * kCounterStride, 0u);
     }
   }
 }
@@ -880,10 +974,18 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
   const uint32_t j = rfl_u32((blockIdx.x >> 3) % ncnt);
   uint32_t* mine = counters + j * kCounterStride;
   const uint64_t nch = nchunks;
+  // start-up as in rmw_kernel: three tickets from one atomic, then both
+  // descriptors loaded together (clamped to a valid index; only tickets below
+  // nchunks are used)
   if (threadIdx.x == 0) {
-    for (int i = 0; i < 3; ++i) sidx[i] = (uint32_t)min((uint64_t)atomicAdd(mine, 1u) * ncnt + j, nch);
-    for (int i = 0; i < 2; ++i)
-      if (sidx[i] < nchunks) sdesc[i] = chunks[sidx[i]];
+    const uint32_t t0 = atomicAdd(mine, 3u);
+    for (int i = 0; i < 3; ++i) sidx[i] = (uint32_t)min((uint64_t)(t0 + i) * ncnt + j, nch);
+    if (nch > 0) {
+      const DzChunk d0 = chunks[min((uint64_t)t0 * ncnt + j, nch - 1)];
+      const DzChunk d1 = chunks[min((uint64_t)(t0 + 1) * ncnt + j, nch - 1)];
+      sdesc[0] = d0;
+      sdesc[1] = d1;
+    }
   }
   __syncthreads();
   for (uint32_t k = 0;; ++k) {
@@ -925,9 +1027,9 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
     __syncthreads();
   }
   if (threadIdx.x == 0) {
-    const uint32_t done = atomicAdd(counters + kCounters * kCounterStride, 1u);
+    const uint32_t done = atomicAdd(counters + kDoneSlot * kCounterStride, 1u);
     if (done == gridDim.x - 1) {
-      for (int i = 0; i <= kCounters; ++i) atomicExch(counters + i * kCounterStride, 0u);
+      for (int i = 0; i <= kDoneSlot; ++i) atomicExch(counters + i * kCounterStride, 0u);
     }
   }
 }
@@ -1062,25 +1164,25 @@ __global__ void __launch_bounds__(256) philox_kernel(uint64_t seed, uint32_t str
   } while (0)
 
 template <int DT>
-static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
+static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t nfull, uint32_t grid,
                                 const void* tab, const DzScalars& s, const DzScalarPtrs& p,
                                 uint32_t* counters, hipStream_t st, const LaunchEvents& ev) {
   switch (mode) {
     case kModePerturb:
       DZ_LAUNCH((rmw_kernel<DT, kModePerturb>), dim3(grid), dim3(kRmwThreads), st, ev,
-                         chunks, nchunks, tab, s, p, counters);
+                         chunks, nchunks, nfull, tab, s, p, counters);
       break;
     case kModeUpdate:
       DZ_LAUNCH((rmw_kernel<DT, kModeUpdate>), dim3(grid), dim3(kRmwThreads), st, ev,
-                         chunks, nchunks, tab, s, p, counters);
+                         chunks, nchunks, nfull, tab, s, p, counters);
       break;
     case kModeRestoreUpdate:
       DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdate>), dim3(grid), dim3(kRmwThreads),
-                         st, ev, chunks, nchunks, tab, s, p, counters);
+                         st, ev, chunks, nchunks, nfull, tab, s, p, counters);
       break;
     case kModeRestoreUpdatePerturb:
       DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdatePerturb>), dim3(grid), dim3(kRmwThreads),
-                         st, ev, chunks, nchunks, tab, s, p, counters);
+                         st, ev, chunks, nchunks, nfull, tab, s, p, counters);
       break;
     default:
       return hipErrorInvalidValue;
@@ -1088,13 +1190,13 @@ static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunk
   return hipGetLastError();
 }
 
-hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
+hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t nfull, uint32_t grid,
                       const void* tab, const DzScalars& s, const DzScalarPtrs& p, uint32_t* counters,
                       hipStream_t st, const LaunchEvents& ev) {
   switch (dtype) {
-    case DZ_F32: return launch_rmw_dt<DZ_F32>(mode, chunks, nchunks, grid, tab, s, p, counters, st, ev);
-    case DZ_F16: return launch_rmw_dt<DZ_F16>(mode, chunks, nchunks, grid, tab, s, p, counters, st, ev);
-    case DZ_BF16: return launch_rmw_dt<DZ_BF16>(mode, chunks, nchunks, grid, tab, s, p, counters, st, ev);
+    case DZ_F32: return launch_rmw_dt<DZ_F32>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, st, ev);
+    case DZ_F16: return launch_rmw_dt<DZ_F16>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, st, ev);
+    case DZ_BF16: return launch_rmw_dt<DZ_BF16>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, st, ev);
     default: return hipErrorInvalidValue;
   }
 }
