@@ -580,17 +580,48 @@ __device__ __forceinline__ void compute_store_tile(const DzChunk& ch, uint32_t g
   }
 }
 
-// Partial or misaligned tile, element by element and bounds-checked: groups
-// first + lane, first + lane + kStride, ... below `end` (and inside the tile).
+// Partial or misaligned tile, bounds-checked: groups first + lane, first +
+// lane + kStride, ... below `end` (and inside the tile). In a 16-byte-aligned
+// tensor a group with all 8 elements inside the tile goes through vector
+// loads and stores like a full tile's; the tensor's last, incomplete group
+// and every group of a misaligned view go element by element.
 template <int DT, int MODE, int kStride>
 __device__ __forceinline__ void rmw_partial(const DzChunk& ch, uint32_t first, uint32_t end, uint32_t lane,
                                             const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc) {
   using S = typename DT_<DT>::S;
   constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
   char* base = (char*)ch.ptr;
+  const bool aligned = (ch.meta & kDzMetaAligned) != 0u;
   for (uint32_t g = first + lane; g < end && g * 8u < ch.n; g += kStride) {
     const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
     const DzU4 w2 = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, ch.zgroup + g) : w;
+    if (aligned && (g + 1u) * 8u <= ch.n) {
+      if constexpr (DT == DZ_F32) {
+        char* p = base + (size_t)g * 32;
+        const dz_u32x4 a = ld_stream(p), b = ld_stream(p + 16);
+        dz_u32x4 o0, o1;
+        o0.x = apply_one<DT, MODE>(a.x, w.x & 0xffffu, w2.x & 0xffffu, tab, sc);
+        o0.y = apply_one<DT, MODE>(a.y, w.x >> 16, w2.x >> 16, tab, sc);
+        o0.z = apply_one<DT, MODE>(a.z, w.y & 0xffffu, w2.y & 0xffffu, tab, sc);
+        o0.w = apply_one<DT, MODE>(a.w, w.y >> 16, w2.y >> 16, tab, sc);
+        o1.x = apply_one<DT, MODE>(b.x, w.z & 0xffffu, w2.z & 0xffffu, tab, sc);
+        o1.y = apply_one<DT, MODE>(b.y, w.z >> 16, w2.z >> 16, tab, sc);
+        o1.z = apply_one<DT, MODE>(b.z, w.w & 0xffffu, w2.w & 0xffffu, tab, sc);
+        o1.w = apply_one<DT, MODE>(b.w, w.w >> 16, w2.w >> 16, tab, sc);
+        st_stream(p, o0);
+        st_stream(p + 16, o1);
+      } else {
+        char* p = base + (size_t)g * 16;
+        const dz_u32x4 v = ld_stream(p);
+        dz_u32x4 o;
+        o.x = combine_pair16<DT, MODE>(v.x, w.x, w2.x, lookup_pair16<DT, MODE>(w.x, w2.x, tab));
+        o.y = combine_pair16<DT, MODE>(v.y, w.y, w2.y, lookup_pair16<DT, MODE>(w.y, w2.y, tab));
+        o.z = combine_pair16<DT, MODE>(v.z, w.z, w2.z, lookup_pair16<DT, MODE>(w.z, w2.z, tab));
+        o.w = combine_pair16<DT, MODE>(v.w, w.w, w2.w, lookup_pair16<DT, MODE>(w.w, w2.w, tab));
+        st_stream(p, o);
+      }
+      continue;
+    }
     const uint32_t m = min(8u, ch.n - g * 8u);
     for (uint32_t j = 0; j < m; ++j) {
       const uint32_t h = (word_of(w, (int)(j >> 1)) >> (16 * (j & 1))) & 0xffffu;

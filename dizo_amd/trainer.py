@@ -422,16 +422,19 @@ class ZOTrainerMixin:
         if pu is not None and s == 1.0 and pu[1] == eps and self._pending_restore is None:
             # previous step's restore + update, then this +1, in one pass
             self._pending_update = None
-            torch.manual_seed(seed)
             tabs = self._zo_tables()
             prev, _, g, lr = pu
             self._launch("restore_update_perturb",
                          lambda t: t.restore_update_perturb(prev, seed, eps, g, lr), tabs)
+            # the reference re-seeds torch's generators here; the kernels do not
+            # use them, so the launch goes first (the GPU waits for it after the
+            # host read projected_grad)
+            torch.manual_seed(seed)
             return
         self.zo_flush()
-        torch.manual_seed(seed)  # the reference re-seeds torch's generators here
         tabs = self._zo_tables()
         self._launch("perturb", lambda t: t.perturb(seed, s, eps), tabs)
+        torch.manual_seed(seed)  # the reference re-seeds torch's generators here
 
     def _prepare_inputs(self, inputs):
         dev = self.named_parameters_to_optim[0][1].device
@@ -471,7 +474,6 @@ class ZOTrainerMixin:
         DiZO event every 50 steps, then the scheduler step."""
         seed = self.zo_random_seed
         torch.manual_seed(seed)
-        tabs = self._zo_tables()
         g, lr = float(self.projected_grad), float(self._get_learning_rate())
         event_due = (self.state.global_step + 1) % DIZO_INTERVAL == 0 and args.enhanced
         pending = self._pending_restore
@@ -481,10 +483,10 @@ class ZOTrainerMixin:
             if getattr(args, "zo_fuse_next_perturb", False) and not event_due:
                 self._pending_update = (seed, eps, g, lr)  # applied with the next +1 perturbation
             else:
-                self._launch("restore_update", lambda t: t.restore_update(seed, eps, g, lr), tabs)
+                self._launch("restore_update", lambda t: t.restore_update(seed, eps, g, lr), self._zo_tables())
         else:
             self.zo_flush()
-            self._launch("update", lambda t: t.update(seed, g, lr), tabs)
+            self._launch("update", lambda t: t.update(seed, g, lr), self._zo_tables())
         if self.zo_journal is not None:
             self.zo_journal.zo(seed, g, lr)
         if event_due:
