@@ -643,10 +643,10 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, uint32_t first, u
 //
 // Wave-level loop (RmwTraits::kSlices): each wave takes slices of 64 * G
 // groups (a sixteenth of a tile; slice id = ticket * K + j from counter j of
-// the K = 16 in use, wave w of workgroup b using counter ((b / 8) * 16 + w)
-// mod K, so every counter serves waves on every XCD) and loads, computes and
-// stores them on its own, with no barrier between slices: while one wave
-// waits for memory, the other waves of its SIMD compute. With a barrier per
+// the K = 16 slice counters, wave w of every workgroup using counter w mod K,
+// so every counter serves waves on every XCD) and loads, computes and stores
+// them on its own, with no barrier between slices: while one wave waits for
+// memory, the other waves of its SIMD compute. With a barrier per
 // tile, all 16 waves of a workgroup load, wait, compute and store in step,
 // and a tile's load latency and its compute add up instead of overlapping.
 //
@@ -666,7 +666,7 @@ __device__ __forceinline__ void rmw_slices(const DzChunk* __restrict__ chunks, u
   static_assert(kSliceCounters <= kRmwThreads / 64, "every slice counter needs a wave of workgroup 0");
   const uint32_t wave = rfl_u32(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t j = rfl_u32(((blockIdx.x >> 3) * kSlices + wave) % ncnt);
+  const uint32_t j = wave % ncnt;
   uint32_t* mine = counters + j * kCounterStride;
   const uint64_t nslices = (uint64_t)nchunks * kSlices;
   TileRegs<DT, MODE> r;

@@ -58,7 +58,7 @@ def test_mixin_in_hf_trainer_matches_zotrainer(enhanced, tmp_path):
     args = OurArguments(output_dir=str(tmp_path), learning_rate=lr, max_steps=steps, report_to=[],
                         enhanced=enhanced, zo_eps=1e-3)
     tr = OurTrainer(model=model_b, args=args)
-    # trainer.py:1099-1101 and 1147-1171, as one call
+    # trainer.py:1099-1101 and 1147-1171 (scheduler, trainable set, anchor, DiZO), as one call
     tr.zo_setup(model_b, Cycle(batches), optimizer=tr.create_optimizer())
     np.random.seed(26)
     got = []
