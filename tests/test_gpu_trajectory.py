@@ -14,7 +14,8 @@ and learning-rate schedule:
     candidates, lengths uniform in [32, 64]): bit for bit against the
     reference's expressions rounded as torch's CPU and CUDA kernels round
     them, with that norm; against ROCm torch's own kernels and torch.norm,
-    within 1e-2 (see the test for why not bit for bit);
+    within 1e-2, and where that run leaves the recipe (fp32 ties that ROCm
+    torch rounds the other way) asserted element by element;
   * config C2 (kernel passes over the OPT-2.7B trainable set): separate
     passes (+1, -2, +1, update) and fused passes give the same weights bit for
     bit, and match the reference's expressions on sampled tensors;
@@ -186,11 +187,12 @@ def test_c3_shape_200_step_loss_trajectory(capsys):
 
     Against ROCm torch's own kernels with torch.norm, the runs separate by a few
     fp16 units of the loss: on some launch paths ROCm torch's fp16
-    `scalar * tensor` kernel rounds exact fp32 ties away from the recipe (14
-    elements of 2,560-element biases at step 35 here). The ZO gradient's fp16
-    quantisation (steps of 0.25 at eps 1e-3) and the gamma search's
-    (L1 - L2) / 0.2 then carry a one-unit weight difference into different
-    updates. That run is reported and bounded at 1e-2."""
+    `scalar * tensor` kernel rounds exact fp32 ties away from the recipe (20
+    elements of 2,560-element tensors in lr * (g * z) at step 35 here,
+    test_c3_rocm_torch_departs_from_the_recipe_only_on_fp32_ties). The ZO
+    gradient's fp16 quantisation (steps of 0.25 at eps 1e-3) and the gamma
+    search's (L1 - L2) / 0.2 then carry a one-unit weight difference into
+    different updates. That run is reported and bounded at 1e-2."""
     from dizo_amd.synth import make_batches
     batches = make_batches(8, 16, 50272, seed=82, device="cuda", min_len=32, max_len=64)
     report = _reporter(capsys)
