@@ -657,6 +657,19 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, uint32_t first, u
 // barrier ends each tile.
 // ---------------------------------------------------------------------------
 template <int DT, int MODE>
+__device__ __forceinline__ void rmw_slice(const DzChunk& ch, uint32_t c, uint32_t nfull, uint32_t first,
+                                          uint32_t lane, TileRegs<DT, MODE>& r,
+                                          const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc) {
+  constexpr uint32_t G = RmwTraits<DT, MODE>::kGroups;
+  if (c < nfull) {
+    load_tile_at<DT, MODE, 64>(ch.ptr, first + lane, r);
+    compute_store_tile<DT, MODE, 64>(ch, first + lane, first, r, tab, sc);
+  } else {
+    rmw_partial<DT, MODE, 64>(ch, first, first + 64u * G, lane, tab, sc);
+  }
+}
+
+template <int DT, int MODE>
 __device__ __forceinline__ void rmw_slices(const DzChunk* __restrict__ chunks, uint32_t nchunks, uint32_t nfull,
                                            const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
                                            uint32_t* __restrict__ counters) {
@@ -676,14 +689,8 @@ __device__ __forceinline__ void rmw_slices(const DzChunk* __restrict__ chunks, u
     const uint64_t sid = (uint64_t)rfl_u32(t) * ncnt + j;  // lane 0 is the first active lane
     if (sid >= nslices) break;
     const uint32_t c = (uint32_t)(sid / kSlices);
-    const uint32_t first = (uint32_t)(sid % kSlices) * 64u * G;
     const DzChunk ch = uniform_chunk(chunks[c]);
-    if (c < nfull) {
-      load_tile_at<DT, MODE, 64>(ch.ptr, first + lane, r);
-      compute_store_tile<DT, MODE, 64>(ch, first + lane, first, r, tab, sc);
-    } else {
-      rmw_partial<DT, MODE, 64>(ch, first, first + 64u * G, lane, tab, sc);
-    }
+    rmw_slice<DT, MODE>(ch, c, nfull, (uint32_t)(sid % kSlices) * 64u * G, lane, r, tab, sc);
   }
 }
 
