@@ -21,7 +21,8 @@ and learning-rate schedule:
     bit, and match the reference's expressions on sampled tensors;
   * config C5's scale (OPT-30B bf16) and config C4, the headline (OPT-13B
     fp16): the fused passes and the projection on sampled tensors and groups
-    against the reference's expressions.
+    against the reference's expressions; at C4 also three whole steps,
+    forwards included, bit for bit.
 """
 import copy
 import sys
@@ -301,6 +302,25 @@ def test_c3_rocm_torch_departs_from_the_recipe_only_on_fp32_ties(capsys):
     for d in deps[:8]:
         print(f"  step {d[0]} {d[1]} {d[2]} ({d[3]} elements): {d[4]}", flush=True)
     assert audit.non_ties == 0
+    tr.zo_close()
+
+
+def test_c4_three_whole_steps_bit_exact():
+    """Config C4, the headline (OPT-13B fp16, 643 tensors, batch 16 x 2 x 128,
+    unpadded): three whole ZO steps of the library trainer, forwards included,
+    against the reference's expressions in the recipe form fed the exported z
+    (trainer.py:1570-1608): the losses and every weight bit for bit."""
+    from dizo_amd.synth import make_batches
+    batches = make_batches(3, 16, 50272, seed=7, device="cuda", fixed_len=128)
+    tr, la, ma, init = _library_run("opt-13b", torch.float16, batches, 3, 1e-6, 1e-3)
+    assert len(tr.named_parameters_to_optim) == 643
+    lb, mb, _ = _reference_run(tr, init, torch.float16, batches, 3, 1e-6, 1e-3, _lib_norm, recipe=True)
+    print("C4 losses:", [float(x) for x in la], flush=True)
+    bad = [k for k, (a, b) in enumerate(zip(la, lb)) if not _same(a, b)]
+    assert not bad, f"losses differ at steps {bad}: {[(float(la[k]), float(lb[k])) for k in bad]}"
+    pb = dict(mb.named_parameters())
+    diff = [n for n, p in ma.named_parameters() if not _same(p.data, pb[n].data)]
+    assert not diff, f"{len(diff)} tensors differ after 3 steps, e.g. {diff[:3]}"
     tr.zo_close()
 
 
