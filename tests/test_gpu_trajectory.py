@@ -21,8 +21,8 @@ and learning-rate schedule:
     bit, and match the reference's expressions on sampled tensors;
   * config C5's scale (OPT-30B bf16) and config C4, the headline (OPT-13B
     fp16): the fused passes and the projection on sampled tensors and groups
-    against the reference's expressions; at C4 also three whole steps,
-    forwards included, bit for bit.
+    against the reference's expressions; at C4 also whole steps, forwards
+    included: three, and fifty ending in a DiZO event, bit for bit.
 """
 import copy
 import sys
@@ -321,6 +321,23 @@ def test_c4_three_whole_steps_bit_exact():
     pb = dict(mb.named_parameters())
     diff = [n for n, p in ma.named_parameters() if not _same(p.data, pb[n].data)]
     assert not diff, f"{len(diff)} tensors differ after 3 steps, e.g. {diff[:3]}"
+    tr.zo_close()
+
+
+def test_c4_fifty_steps_with_a_dizo_event_bit_exact(capsys):
+    """Config C4 over 50 steps, the last one ending in a DiZO event (10 SPSA
+    iterations on the 80 k/v gammas, 20 forwards, the final apply;
+    trainer.py:1611-1615, 782-803): the library trainer against the
+    reference's expressions in the recipe form with the library's norm
+    definition, fed the exported z and gamma noise: losses, gamma and every
+    weight bit for bit."""
+    from dizo_amd.synth import make_batches
+    batches = make_batches(4, 16, 50272, seed=11, device="cuda", fixed_len=128)
+    report = _reporter(capsys)
+    tr, la, ma, init = _library_run("opt-13b", torch.float16, batches, 50, 1e-6, 1e-3, progress=report)
+    lb, mb, gb = _reference_run(tr, init, torch.float16, batches, 50, 1e-6, 1e-3, _lib_norm, recipe=True,
+                                progress=report)
+    _assert_bit_exact(tr, la, ma, lb, mb, gb)
     tr.zo_close()
 
 
