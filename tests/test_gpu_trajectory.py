@@ -21,8 +21,8 @@ and learning-rate schedule:
     bit, and match the reference's expressions on sampled tensors;
   * config C5's scale (OPT-30B bf16) and config C4, the headline (OPT-13B
     fp16): the fused passes and the projection on sampled tensors and groups
-    against the reference's expressions; at C4 also whole steps, forwards
-    included: three, and fifty ending in a DiZO event, bit for bit.
+    against the reference's expressions; whole steps, forwards included, bit
+    for bit: at C4 three, and fifty ending in a DiZO event; at C5 two.
 """
 import copy
 import sys
@@ -338,6 +338,52 @@ def test_c4_fifty_steps_with_a_dizo_event_bit_exact(capsys):
     lb, mb, gb = _reference_run(tr, init, torch.float16, batches, 50, 1e-6, 1e-3, _lib_norm, recipe=True,
                                 progress=report)
     _assert_bit_exact(tr, la, ma, lb, mb, gb)
+    tr.zo_close()
+
+
+def test_c5_two_whole_steps_bit_exact():
+    """Config C5 (OPT-30B bf16, 771 tensors, 29.6 G elements, batch 8 x 2 x
+    256, unpadded): two whole ZO steps of the library trainer, forwards
+    included (its three-way pass on the wave-slice loop), against the
+    reference's expressions in the recipe form fed the exported z, one tensor
+    at a time (three 59 GB copies of the model fit; a fourth would not): the
+    losses and every weight bit for bit."""
+    from dizo_amd.synth import make_batches
+    from dizo_amd.trainer import select_trainable
+    dt, steps, lr0, eps = torch.bfloat16, 2, 1e-6, 1e-3
+    batches = make_batches(steps, 8, 50272, seed=13, device="cuda", fixed_len=256)
+    tr, la, ma, init = _library_run("opt-30b", dt, batches, steps, lr0, eps)
+    named, _ = select_trainable(init)
+    assert len(named) == 771
+    names = [n for n, _ in named]
+    params = [p for _, p in named]  # the copy of the initial model becomes the reference side
+    np.random.seed(26)
+
+    def each(op, seed, *args):
+        for n, p in zip(names, params):
+            z = tr.export_z(n, seed)
+            op([p], [z], *args)
+            del z
+
+    lb = []
+    for k in range(steps):
+        seed = np.random.randint(1000000000)
+        batch = batches[k]
+        each(R.zo_perturb_parameters_recipe, seed, 1, eps)
+        l1 = _ref_forward(init, batch)
+        each(R.zo_perturb_parameters_recipe, seed, -2, eps)
+        l2 = _ref_forward(init, batch)
+        g = R.projected_grad(l1, l2, eps)
+        each(R.zo_perturb_parameters_recipe, seed, 1, eps)
+        each(R.zo_update_recipe, seed, g, A.zo_lr(lr0, k, steps))
+        lb.append(l1)
+    torch.cuda.synchronize()
+    print("C5 losses:", [float(x) for x in la], flush=True)
+    bad = [k for k, (a, b) in enumerate(zip(la, lb)) if not _same(a, b)]
+    assert not bad, f"losses differ at steps {bad}: {[(float(la[k]), float(lb[k])) for k in bad]}"
+    pb = dict(init.named_parameters())
+    diff = [n for n, p in ma.named_parameters() if not _same(p.data, pb[n].data)]
+    assert not diff, f"{len(diff)} tensors differ after {steps} steps, e.g. {diff[:3]}"
     tr.zo_close()
 
 
