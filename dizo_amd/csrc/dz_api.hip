@@ -243,6 +243,17 @@ dz::LaunchEvents take_timing(dz_table* t) {
   return ev;
 }
 
+// A call with nothing to launch records its timing pair back to back on the
+// stream, so the pair still brackets the call's (empty) device work.
+int32_t record_unlaunched(const dz::LaunchEvents& ev, void* stream) {
+  for (hipEvent_t e : {ev.start, ev.stop}) {
+    if (!e) continue;
+    const hipError_t r = hipEventRecord(e, (hipStream_t)stream);
+    if (r != hipSuccess) return hip_fail(r, "hipEventRecord (timing of a call with nothing to launch)");
+  }
+  return DZ_OK;
+}
+
 int32_t check_table(const dz_table* t) {
   if (!t) return fail(DZ_ERR_INVALID, "table is NULL");
   int dev;
@@ -305,7 +316,7 @@ int32_t rmw(dz_table* t, int mode, const dz::DzScalars& s, const dz::DzScalarPtr
     ntiles = t->extra.n;
     nfull = t->extra.nfull;
   }
-  if (ntiles == 0) return DZ_OK;
+  if (ntiles == 0) return record_unlaunched(ev, stream);
   hipError_t e = dz::launch_rmw(t->dtype, mode, chunks, ntiles, nfull, rmw_grid(t, mode, ntiles),
                                 t->dev->tab[t->dtype], s, p, t->d_counters, (hipStream_t)stream, ev);
   if (e != hipSuccess) return hip_fail(e, "rmw kernel launch");
@@ -778,13 +789,12 @@ int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sum
                                    d_alpha, t->d_partials, t->d_counters, (hipStream_t)stream,
                                    {ev.start, finalize ? nullptr : ev.stop});
     if (e != hipSuccess) return hip_fail(e, "projection kernel launch");
-    ev.start = nullptr;
+    ev = {nullptr, finalize ? ev.stop : nullptr};
   }
-  if (finalize) {
-    hipError_t e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_sumsq,
-                                       d_norm_f32, d_norm_T, true, (hipStream_t)stream, ev);
-    if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
-  }
+  if (!finalize) return record_unlaunched(ev, stream);
+  hipError_t e = dz::launch_finalize(t->dtype, t->d_partials, t->d_group_begin, (uint32_t)t->n, d_sumsq, d_norm_f32,
+                                     d_norm_T, true, (hipStream_t)stream, ev);
+  if (e != hipSuccess) return hip_fail(e, "finalize kernel launch");
   return DZ_OK;
 }
 

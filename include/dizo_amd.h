@@ -88,8 +88,10 @@ int32_t dz_table_z_offset(const dz_table* t, int32_t idx, uint64_t* out);
  * and stop_event when its last kernel ends, through hipExtLaunchKernel, so
  * the pair times the kernels without the host's launch work. Either may be
  * NULL. Both are hipEvent_t handles the caller created (and has recorded at
- * least once). The request is taken by that next call, whether or not it
- * launches; do not set it on a stream being captured into a graph. */
+ * least once). The request is taken by that next call: one with nothing to
+ * launch (every tensor empty) records both on its stream at once, one that
+ * fails records neither. Do not set it on a stream being captured into a
+ * graph. */
 int32_t dz_table_time_next(dz_table* t, void* start_event, void* stop_event);
 
 /* ---- ZO step (trainer.py:1429-1444, 1570-1617) -------------------------- */

@@ -125,3 +125,28 @@ def test_time_next_rejects_events_that_do_not_exist_yet():
     with pytest.raises(L.DzError):
         t.time_next(e, None)
     t.close()
+
+
+def test_calls_with_nothing_to_launch_record_their_events():
+    """A table of empty tensors launches no kernel; the requested events are
+    then recorded on the stream at the call (elapsed time about zero, after
+    a slow kernel queued before it)."""
+    z = ZOTable([torch.empty(0, dtype=torch.float16, device="cuda")])
+    e = torch.empty(0, dtype=torch.float16, device="cuda")
+    p = ProjTable([e], [e.clone()])
+    alpha = torch.ones(1, dtype=torch.float16, device="cuda")
+    big = torch.randn(1 << 26, device="cuda")
+    for call, tab in ((lambda: z.perturb(3, 1.0, 1e-3), z), (lambda: p.project(alpha, L.DZ_PROJ_APPLY), p)):
+        torch.cuda.synchronize()
+        e0, e1 = _created_events()
+        torch.cuda.synchronize()
+        tab.time_next(e0, e1)
+        before = torch.cuda.Event(enable_timing=True)
+        before.record()
+        big.mul_(1.0)  # device work queued before the call
+        call()
+        torch.cuda.synchronize()
+        assert before.elapsed_time(e0) > 0  # recorded at the call, after the queued work
+        assert 0 <= e0.elapsed_time(e1) < 0.05
+    z.close()
+    p.close()
