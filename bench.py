@@ -99,7 +99,7 @@ def event_offset(steps: int, warmup: int, interval: int = 50) -> int:
 
 
 def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = False, option_head: bool = False,
-              enhanced: str = "zo", fused: bool = False, attention: bool = False):
+              enhanced: str = "zo", fused: bool = False, attention: bool = False, host_grad: bool = False):
     import numpy as np
     import torch
 
@@ -120,7 +120,8 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = Fa
     offset = event_offset(steps, warmup, DIZO_INTERVAL) if enhanced != "none" else 0
     args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=offset + warmup + steps,
                        enhanced=None if enhanced == "none" else enhanced, zo_graph=graph, zo_option_head=option_head,
-                       zo_fused_mlp=fused, zo_fused_qkv=fused, zo_fused_attention=fused and attention)
+                       zo_fused_mlp=fused, zo_fused_qkv=fused, zo_fused_attention=fused and attention,
+                       zo_host_grad=host_grad)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches), base_model=base)
     # start the step counter at `offset` (the LR schedule follows it, trainer.py:1100-1102)
@@ -567,6 +568,9 @@ def main(argv=None):
                     help="with the fused layers, run an unpadded batch's causal attention through the library's "
                          "MFMA kernel (within SDPA's rounding, not bit for bit; default: SDPA)")
     ap.add_argument("--sdpa", action="store_true", help="SDPA's attention (the default; kept for old command lines)")
+    ap.add_argument("--host-grad", action="store_true",
+                    help="read projected_grad back to the host in every step, as the reference does (default: the "
+                         "kernels read it on the device and the step has no synchronisation; the same values)")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the DiZO step path is measured on a "
@@ -600,7 +604,7 @@ def main(argv=None):
         return 0
     use_dz_attention = a.dz_attention and not a.hf_layers and not a.sdpa
     r = run_steps(a.workload, a.steps, a.warmup, log=log, graph=a.graph, option_head=not a.full_logits,
-                  enhanced=a.enhanced, fused=not a.hf_layers, attention=use_dz_attention)
+                  enhanced=a.enhanced, fused=not a.hf_layers, attention=use_dz_attention, host_grad=a.host_grad)
     wl = WORKLOADS[a.workload]
     value, zo_rate, event_s = amortised(a.steps, r["elapsed"], r["event_s"])
     summ = r["summary"]
@@ -633,7 +637,7 @@ def main(argv=None):
                    "first_global_step": r["offset"],
                    "graph": a.graph, "option_head": not a.full_logits, "fused_gemms": not a.hf_layers,
                    "attention": "dz_attention_causal (unpadded batches)" if use_dz_attention else "sdpa",
-                   "enhanced": a.enhanced,
+                   "enhanced": a.enhanced, "projected_grad": "host (.item())" if a.host_grad else "device",
                    "seq_len": wl["fixed_len"] or wl["max_len"],
                    "device": {"name": torch.cuda.get_device_name(0),
                               "compute_units": torch.cuda.get_device_properties(0).multi_processor_count}},

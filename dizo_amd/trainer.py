@@ -80,6 +80,12 @@ class ZOArguments:
     # the first perturbation of the next zo_step
     zo_fuse_restore: bool = True
     zo_fuse_next_perturb: bool = True
+    # build-specific: read projected_grad back to the host in every zo_step,
+    # as trainer.py:1587 does (.item()). By default the quotient stays on the
+    # device, the kernels read it there, and the host reads it only when the
+    # attribute is asked for: the step then has no synchronisation and the
+    # next pass queues behind the second forward (same values bit for bit)
+    zo_host_grad: bool = False
     # build-specific: replay each step as a captured hipGraph (ZOTrainer only)
     zo_graph: bool = False
     # build-specific: compute logits only at the option positions the
@@ -304,6 +310,12 @@ class _ZOTables:
         self.tables = []
 
 
+def _grad_args(g):
+    """(value, device scalar) arguments of a table call for a projected
+    gradient held as a float or as a device scalar of the table's dtype."""
+    return (0.0, g) if torch.is_tensor(g) else (float(g), None)
+
+
 class ZOTrainerMixin:
     """The reference's ZO step methods, running on the library's kernels.
 
@@ -373,6 +385,36 @@ class ZOTrainerMixin:
     def _get_learning_rate(self) -> float:
         return self.lr_scheduler.get_last_lr()[0]
 
+    @property
+    def projected_grad(self):
+        """trainer.py:1587: ((loss1 - loss2) / (2 * zo_eps)).item(), a Python
+        float. zo_step may keep the quotient as a device scalar (see
+        ZOArguments.zo_host_grad); reading the attribute then synchronises
+        once and keeps the float."""
+        g = self.__dict__.get("_projected_grad")
+        if torch.is_tensor(g):
+            g = float(g.item())
+            self.__dict__["_projected_grad"] = g
+        return g
+
+    @projected_grad.setter
+    def projected_grad(self, value) -> None:
+        self.__dict__["_projected_grad"] = value
+
+    def _grad_value(self):
+        """The projected gradient as zo_step left it: a float, or a device
+        scalar of the ZO tables' dtype that the kernels read in place."""
+        return self.__dict__.get("_projected_grad")
+
+    def _device_grad_ok(self, g: torch.Tensor) -> bool:
+        """Whether the kernels can read g where it is: one element of every ZO
+        table's dtype, on their device. The reference's g is the loss's value
+        (a value of the loss dtype), and the kernels read a device g as a value
+        of T, so this holds exactly when the loss dtype is T."""
+        if getattr(self.args, "zo_host_grad", False) or g.numel() != 1:
+            return False
+        return all(t.dtype == g.dtype and t.device == g.device for t, _ in self._zo_tables().tables)
+
     def _zo_tables(self) -> _ZOTables:
         tabs = self._zo_tabs
         if tabs is None or tabs.stale():
@@ -404,8 +446,9 @@ class ZOTrainerMixin:
         if pu is not None:
             self._pending_update = None
             seed, eps, g, lr = pu
+            gv, gd = _grad_args(g)
             tabs = self._zo_tables()
-            self._launch("restore_update", lambda t: t.restore_update(seed, eps, g, lr), tabs)
+            self._launch("restore_update", lambda t: t.restore_update(seed, eps, gv, lr, d_grad=gd), tabs)
         pending = self._pending_restore
         if pending is not None:
             self._pending_restore = None
@@ -424,11 +467,11 @@ class ZOTrainerMixin:
             self._pending_update = None
             tabs = self._zo_tables()
             prev, _, g, lr = pu
+            gv, gd = _grad_args(g)
             self._launch("restore_update_perturb",
-                         lambda t: t.restore_update_perturb(prev, seed, eps, g, lr), tabs)
+                         lambda t: t.restore_update_perturb(prev, seed, eps, gv, lr, d_grad=gd), tabs)
             # the reference re-seeds torch's generators here; the kernels do not
-            # use them, so the launch goes first (the GPU waits for it after the
-            # host read projected_grad)
+            # use them, so the launch goes first
             torch.manual_seed(seed)
             return
         self.zo_flush()
@@ -461,7 +504,10 @@ class ZOTrainerMixin:
         self.zo_perturb_parameters(scaling_factor=-2)
         loss2 = self.zo_forward(model, inputs)
         self._last_loss2 = loss2
-        self.projected_grad = ((loss1 - loss2) / (2 * self.args.zo_eps)).item()
+        g = (loss1 - loss2) / (2 * self.args.zo_eps)
+        # trainer.py:1587 reads g back here (.item()); kept on the device, the
+        # host does not wait for the second forward (see projected_grad)
+        self.projected_grad = g if self._device_grad_ok(g) else g.item()
         assert self.args.gradient_accumulation_steps == 1
         if getattr(args, "zo_fuse_restore", True):
             self._pending_restore = (self.zo_random_seed, float(args.zo_eps))
@@ -474,7 +520,8 @@ class ZOTrainerMixin:
         DiZO event every 50 steps, then the scheduler step."""
         seed = self.zo_random_seed
         torch.manual_seed(seed)
-        g, lr = float(self.projected_grad), float(self._get_learning_rate())
+        g, lr = self._grad_value(), float(self._get_learning_rate())
+        gv, gd = _grad_args(g)
         event_due = (self.state.global_step + 1) % DIZO_INTERVAL == 0 and args.enhanced
         pending = self._pending_restore
         if pending is not None and pending[0] == seed:
@@ -483,10 +530,11 @@ class ZOTrainerMixin:
             if getattr(args, "zo_fuse_next_perturb", False) and not event_due:
                 self._pending_update = (seed, eps, g, lr)  # applied with the next +1 perturbation
             else:
-                self._launch("restore_update", lambda t: t.restore_update(seed, eps, g, lr), self._zo_tables())
+                self._launch("restore_update", lambda t: t.restore_update(seed, eps, gv, lr, d_grad=gd),
+                             self._zo_tables())
         else:
             self.zo_flush()
-            self._launch("update", lambda t: t.update(seed, g, lr), self._zo_tables())
+            self._launch("update", lambda t: t.update(seed, gv, lr, d_grad=gd), self._zo_tables())
         if self.zo_journal is not None:
             self.zo_journal.zo(seed, g, lr)
         if event_due:
@@ -614,7 +662,7 @@ class ZOTrainer(ZOTrainerMixin):
         self._account(tr_loss_step)
         lr = self._get_learning_rate()
         self.zo_update(self.args, model)
-        self._log_step(tr_loss_step, self._last_loss2, self.projected_grad, lr)
+        self._log_step(tr_loss_step, self._last_loss2, self._grad_value(), lr)
         self._finish_step(tr_loss_step)
         return tr_loss_step
 

@@ -367,16 +367,20 @@ def test_dizo_first_order_iterations_within_the_fp32_sum_bound(dt):
     dtr.close()
 
 
-def _run_trainer(dt, graph, enhanced, steps, batches, seed=31, option_head=False):
+def _run_trainer(dt, graph, enhanced, steps, batches, seed=31, option_head=False, grads=None, **kw):
     from dizo_amd.synth import Cycle, build_opt
     from dizo_amd.trainer import ZOArguments, ZOTrainer
     model = build_opt("opt-tiny", dt, "cuda", seed=seed)
     args = ZOArguments(learning_rate=1e-3, zo_eps=1e-3, max_steps=steps, enhanced=enhanced, zo_graph=graph,
-                       zo_option_head=option_head)
+                       zo_option_head=option_head, **kw)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches))
     it = iter(Cycle(batches))
-    losses = [tr.training_step(next(it)) for _ in range(steps)]
+    losses = []
+    for _ in range(steps):
+        losses.append(tr.training_step(next(it)))
+        if grads is not None:
+            grads.append(tr._grad_value())
     tr.zo_close()
     torch.cuda.synchronize()
     return torch.stack([l.reshape(()) for l in losses]), [p.detach().clone() for p in model.parameters()]
@@ -406,6 +410,44 @@ def test_graph_steps_with_dizo_event_match_eager():
     lg, pg = _run_trainer(torch.float16, True, "zo", 55, batches)
     assert _same(le, lg)
     assert all(_same(a, b) for a, b in zip(pe, pg))
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_device_grad_matches_host_grad(dt):
+    """zo_step keeps projected_grad on the device, where the kernels read it
+    (no synchronisation in the step), unless zo_host_grad asks for the
+    reference's .item() in every step (trainer.py:1587). 55 steps with a
+    DiZO event at global step 49 give the same losses and parameters bit for
+    bit either way, and every step's gradient is the same value."""
+    from dizo_amd.synth import make_batches
+    batches = make_batches(5, 4, 512, seed=44, device="cuda", min_len=8, max_len=20)
+    g_dev, g_host = [], []
+    ld, pd = _run_trainer(dt, False, "zo", 55, batches, grads=g_dev)
+    lh, ph = _run_trainer(dt, False, "zo", 55, batches, grads=g_host, zo_host_grad=True)
+    assert all(torch.is_tensor(g) and g.dtype == dt and g.numel() == 1 for g in g_dev)
+    assert all(isinstance(g, float) for g in g_host)
+    assert [float(g.item()) for g in g_dev] == g_host
+    assert _same(ld, lh), f"losses differ: {ld} vs {lh}"
+    assert all(_same(a, b) for a, b in zip(pd, ph))
+
+
+def test_projected_grad_attribute_reads_back_a_float():
+    """The attribute a caller of the reference reads is a Python float, also
+    when the step kept it on the device; reading it keeps the float."""
+    from dizo_amd.synth import build_opt, make_batches
+    from dizo_amd.trainer import ZOArguments, ZOTrainer
+    model = build_opt("opt-tiny", torch.float16, "cuda", seed=5)
+    batches = make_batches(2, 4, 512, seed=45, device="cuda", fixed_len=16)
+    np.random.seed(26)
+    tr = ZOTrainer(model, ZOArguments(learning_rate=1e-3, zo_eps=1e-3, max_steps=4))
+    tr.zo_step(model, batches[0])
+    held = tr._grad_value()
+    assert torch.is_tensor(held)
+    g = tr.projected_grad
+    assert isinstance(g, float) and g == float(held.item())
+    assert tr._grad_value() == g  # kept as the float
+    tr.zo_update(tr.args, model)
+    tr.zo_close()
 
 
 def _ulp(x: float, dt) -> float:
