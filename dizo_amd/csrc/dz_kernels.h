@@ -81,15 +81,27 @@ __host__ __device__ constexpr int rmw_lds_table_bytes(int dtype, int mode) {
 // launch puts them back to zero, so consecutive launches on one stream need
 // no reset (and no memset in a captured graph). Launches of one table must
 // not overlap in time.
-// RMW launches that run the wave-level loop: bit 4 * dtype + mode (dtype
-// DZ_F32 0, DZ_F16 1, DZ_BF16 2; mode as RmwMode); the others run the
-// workgroup-level loop. Measured on the MI355X: the wave-level loop is
-// faster only for the bf16 restore+update+next perturb pass (OPT-30B: 22.9
-// against 24.0 ms), whose ALU work per tile is the largest; every streaming
-// pass runs slower with it (OPT-13B fp16 perturb 7.92 against 7.71 ms,
-// OPT-125m fp32 0.149 against 0.125 ms).
+// Tile loops of the RMW launches, by bit 4 * dtype + mode (dtype DZ_F32 0,
+// DZ_F16 1, DZ_BF16 2; mode as RmwMode):
+//   DZ_RMW_PREFETCH_MASK: the workgroup-level loop that loads the next full
+//     tile while it computes the current one (rmw_tiles_prefetch). Measured
+//     on the MI355X, same box, alternating builds: the restore+update+next
+//     perturb passes, whose ALU work per tile is the largest, gain (OPT-13B
+//     fp16 8.15-8.18 -> 7.97 ms, OPT-30B bf16 22.5-23.0 -> 20.4-20.6 ms);
+//     every single-Philox pass loses (OPT-13B fp16 perturb 7.66 -> 8.86 ms,
+//     OPT-30B bf16 17.8 -> 21.0 ms), and so does the fp32 three-way pass
+//     (OPT-125m 0.121 -> 0.126 ms), so those keep the plain loop.
+//   DZ_RMW_SLICE_MASK: the wave-level loop (rmw_slices), no barrier between
+//     slices. Before the prefetching loop it was the faster form of the bf16
+//     three-way pass (OPT-30B 22.9 against 24.0 ms); every streaming pass
+//     runs slower with it (OPT-13B fp16 perturb 7.92 against 7.71 ms,
+//     OPT-125m fp32 0.149 against 0.125 ms). Now off by default.
+// Both can be set per mode with -D; the slice loop takes precedence.
+#ifndef DZ_RMW_PREFETCH_MASK
+#define DZ_RMW_PREFETCH_MASK ((1 << (4 * 1 + 3)) | (1 << (4 * 2 + 3)))
+#endif
 #ifndef DZ_RMW_SLICE_MASK
-#define DZ_RMW_SLICE_MASK (1 << (4 * 2 + 3))
+#define DZ_RMW_SLICE_MASK 0
 #endif
 constexpr int kCounters = DZ_RMW_COUNTERS;
 constexpr int kSliceCounters = 16;

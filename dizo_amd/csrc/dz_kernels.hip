@@ -138,6 +138,7 @@ struct RmwTraits {
   // two workgroups share a CU (64 VGPRs).
   static constexpr int kWavesPerEU = (kWide || DZ_RMW_NARROW_WG_PER_CU == 1) ? 4 : 8;
   static constexpr bool kSlices = ((DZ_RMW_SLICE_MASK >> (4 * DT + MODE)) & 1) != 0;
+  static constexpr bool kPrefetch = !kSlices && ((DZ_RMW_PREFETCH_MASK >> (4 * DT + MODE)) & 1) != 0;
 };
 
 // Table entry for z = +Q_T[i] (qbits = bits of Q_T[i]).
@@ -433,6 +434,49 @@ __device__ __forceinline__ uint64_t rfl_u64(uint64_t x) {
   return ((uint64_t)rfl_u32((uint32_t)(x >> 32)) << 32) | (uint64_t)rfl_u32((uint32_t)x);
 }
 
+// Workgroup barrier that orders LDS accesses only. __syncthreads() is a
+// barrier between release and acquire fences on every address space, so
+// before the barrier each wave waits for all of its vector-memory operations
+// (s_waitcnt vmcnt(0)), its global stores included. The projection kernel's
+// barriers only hand over LDS state (the chunk and descriptor rings, the
+// reduction slots), and its chunks' stores need no ordering with the other
+// waves (chunks are disjoint and nothing in the launch reads them back), so
+// its barriers wait for the LDS counter alone. (Measured at OPT-13B: the
+// reverse + norm pass, whose reduction barrier comes after the chunk's
+// stores, 1.98 -> 1.91 ms; the other projection passes unchanged. The RMW
+// kernel's tile loop measured no faster with the same change, since a tile's
+// loads complete behind the previous tile's stores either way, so it keeps
+// __syncthreads().)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Work tickets of the projection kernel's loop: lane 0 takes the next index
+// from a work counter with a returning vector atomic add, issued as an
+// instruction of its own so that the compiler's wait-counter bookkeeping does
+// not track it, and ticket_wait<N> waits for it explicitly once N more
+// vector-memory operations have been issued behind it (the chunk's loads and
+// stores). Tracked by the compiler, the ticket's result, used at the end of
+// the chunk and merged across the full and partial chunk paths, would be
+// waited for with a wait for every operation in flight. Hidden from the
+// compiler, the ticket only ever makes the compiler's own waits wait for one
+// operation more than they count, never less: vector-memory operations leave
+// the wait counter in issue order.
+__device__ __forceinline__ uint32_t ticket_take(uint32_t* counter) {
+  uint32_t t;
+  asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=&v"(t) : "v"(counter), "v"(1u) : "memory");
+  return t;
+}
+// Waits until at most N vector-memory operations are in flight: the ticket,
+// issued before at least N operations that follow it, has returned.
+template <int N>
+__device__ __forceinline__ void ticket_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // A chunk descriptor read from LDS is the same for every lane: move it to
 // scalar registers so tile addresses are formed once per wave.
 __device__ __forceinline__ DzChunk uniform_chunk(const DzChunk& c) {
@@ -695,13 +739,13 @@ __device__ __forceinline__ void rmw_slices(const DzChunk* __restrict__ chunks, u
 }
 
 template <int DT, int MODE>
-__device__ __forceinline__ void rmw_tiles(const DzChunk* __restrict__ chunks, uint32_t nchunks,
+__device__ __forceinline__ void rmw_tiles(uint32_t k0, const DzChunk* __restrict__ chunks, uint32_t nchunks,
                                           const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
                                           uint32_t* sidx, DzChunk* sdesc, uint32_t* mine, uint32_t ncnt,
                                           uint32_t j) {
   const uint64_t nch = nchunks;
   TileRegs<DT, MODE> cur;
-  for (uint32_t k = 0;; ++k) {
+  for (uint32_t k = k0;; ++k) {
     const uint32_t c = sidx[k % 4];
     if (c >= nchunks) break;
     const DzChunk ch = uniform_chunk(sdesc[k % 3]);
@@ -743,6 +787,111 @@ __device__ __forceinline__ void rmw_tiles(const DzChunk* __restrict__ chunks, ui
     }
     __syncthreads();
   }
+}
+
+// Whether the Philox counters of a full tile's groups share their high word
+// (the low word does not wrap inside the tile).
+template <int DT, int MODE>
+__device__ __forceinline__ bool tile_counters_share_high_word(const DzChunk& ch) {
+  constexpr uint32_t kSpan = (uint32_t)(RmwTraits<DT, MODE>::kGroups * kRmwThreads);
+  return (uint32_t)ch.zgroup <= 0xffffffffu - (kSpan - 1u);
+}
+
+// A wait for every vector-memory operation in flight that the compiler sees
+// (s_waitcnt with vmcnt 0 and the other counters at their maximum, gfx9
+// encoding), so its own bookkeeping knows that nothing is pending after it.
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// One tile of the prefetching tile loop (see rmw_tiles_prefetch): full tile
+// k is computed from `cur` (loaded during tile k - 1) while tile k + 1 is
+// loaded into `nxt`. Returns whether tile k + 1 is a full tile (its data is
+// then in `nxt`); if it is not, the loads read a stand-in of the same size
+// (the quantile table), so that every path issues the same loads.
+template <int DT, int MODE>
+__device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk* __restrict__ chunks, uint32_t nchunks,
+                                                  const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
+                                                  uint32_t* sidx, DzChunk* sdesc, uint32_t* mine, uint32_t ncnt,
+                                                  uint32_t j, const void* dummy, const TileRegs<DT, MODE>& cur,
+                                                  TileRegs<DT, MODE>& nxt) {
+  constexpr int kVecs = TileRegs<DT, MODE>::kVecs;
+  const DzChunk ch = uniform_chunk(sdesc[k % 3]);
+  const uint32_t c1 = rfl_u32(sidx[(k + 1) % 4]);
+  const DzChunk ch1 = uniform_chunk(sdesc[(k + 1) % 3]);
+  const bool nxt_full = c1 < nchunks && full_tile<DT, MODE>(ch1) && tile_counters_share_high_word<DT, MODE>(ch1);
+  const uint64_t nptr = nxt_full ? ch1.ptr : (uint64_t)(uintptr_t)dummy;
+  // wave 0: the ticket of tile k + 3 and the descriptor of tile k + 2
+  uint32_t grabbed = 0;
+  uint64_t n_ptr = 0, n_zg = 0;
+  uint32_t n_n = 0, n_meta = 0;
+  bool have_desc = false;
+  if ((rfl_u32(threadIdx.x) >> 6) == 0) {  // wave 0 (uniform branch)
+    if (threadIdx.x == 0) grabbed = ticket_take(mine);
+    const uint32_t cd = rfl_u32(sidx[(k + 2) % 4]);
+    if (cd < nchunks) {
+      const DzChunk* src = chunks + cd;
+      n_ptr = src->ptr;
+      n_zg = src->zgroup;
+      n_n = src->n;
+      n_meta = src->meta;
+      have_desc = true;
+    }
+  }
+  load_tile_at<DT, MODE, kRmwThreads>(nptr, threadIdx.x, nxt);
+  __builtin_amdgcn_sched_barrier(0);
+  tile_body<DT, MODE, true, kRmwThreads>(ch, threadIdx.x, cur, tab, sc);
+  if (threadIdx.x == 0) {
+    ticket_wait<2 * kVecs>();  // behind the ticket: tile k + 1's loads and tile k's stores
+    sidx[(k + 3) % 4] = (uint32_t)min((uint64_t)grabbed * ncnt + j, (uint64_t)nchunks);
+    if (have_desc) {
+      DzChunk& d = sdesc[(k + 2) % 3];
+      d.ptr = n_ptr;
+      d.aux = 0;
+      d.zgroup = n_zg;
+      d.n = n_n;
+      d.meta = n_meta;
+    }
+  }
+  lds_barrier();
+  return nxt_full;
+}
+
+// Tile loop with the next tile's loads in flight during each tile's work,
+// over the run of full tiles a workgroup takes first (a table lists its full
+// tiles first); the rest of its tiles go through rmw_tiles. Two register
+// sets are used in turn (the loop unrolled by two, so no pending registers
+// are copied); each step is one straight block whose loads go out ahead of
+// the Philox chains; the ticket is hidden from the compiler (ticket_take); and
+// the barrier orders LDS only. With those, the compiler's waits for a tile's
+// data count the operations behind it (the previous tile's stores and the
+// next tile's loads) instead of draining everything in flight.
+template <int DT, int MODE>
+__device__ __forceinline__ uint32_t rmw_tiles_prefetch(const DzChunk* __restrict__ chunks, uint32_t nchunks,
+                                                       const typename RmwTraits<DT, MODE>::E* tab,
+                                                       const DzScalars& sc, uint32_t* sidx, DzChunk* sdesc,
+                                                       uint32_t* mine, uint32_t ncnt, uint32_t j,
+                                                       const void* dummy) {
+  const uint32_t c0 = rfl_u32(sidx[0]);
+  const DzChunk ch0 = uniform_chunk(sdesc[0]);
+  if (!(c0 < nchunks && full_tile<DT, MODE>(ch0) && tile_counters_share_high_word<DT, MODE>(ch0))) return 0;
+  // the stand-in must hold a whole tile (a thread's last vector ends at the
+  // tile's size)
+  static_assert(RmwTraits<DT, MODE>::kChunk <= kDzTabEntries, "the quantile table is a tile's stand-in");
+  TileRegs<DT, MODE> a, b;
+  load_tile_at<DT, MODE, kRmwThreads>(ch0.ptr, threadIdx.x, a);
+  uint32_t k = 0;
+  for (;;) {
+    if (!rmw_prefetch_step<DT, MODE>(k, chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j, dummy, a, b)) {
+      k += 1;
+      break;
+    }
+    if (!rmw_prefetch_step<DT, MODE>(k + 1, chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j, dummy, b, a)) {
+      k += 2;
+      break;
+    }
+    k += 2;
+  }
+  wait_vm_all();  // the stand-in loads of the last step
+  return k;
 }
 
 template <int DT, int MODE>
@@ -795,7 +944,9 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
     }
     store_table<DT, MODE>(tab, qs, sc);
     __syncthreads();
-    rmw_tiles<DT, MODE>(chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j);
+    uint32_t k0 = 0;
+    if constexpr (Tr::kPrefetch) k0 = rmw_tiles_prefetch<DT, MODE>(chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j, qtab);
+    rmw_tiles<DT, MODE>(k0, chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j);
   }
   if (threadIdx.x == 0) {
     const uint32_t done = atomicAdd(counters + kDoneSlot * kCounterStride, 1u);
@@ -906,13 +1057,26 @@ __device__ __forceinline__ double block_sum_f64(double x, double* red) {
   for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
   const int wid = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) red[wid] = x;
-  __syncthreads();
+  lds_barrier();
   double t = 0.0;
   if (threadIdx.x == 0) {
     for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t += red[i];
   }
   return t;
 }
+
+// A chunk the vector path takes whole: full size and 16-byte aligned.
+__device__ __forceinline__ bool proj_full_chunk(const DzChunk& ch) {
+  return ch.n == (uint32_t)kProjChunk && (ch.meta & kDzMetaAligned) != 0u;
+}
+
+// Vector-memory operations a thread issues for a full chunk: its 16-byte
+// loads of theta and theta0, and its stores of theta (none for SUMSQ).
+template <int DT, int MODE>
+struct ProjChunkOps {
+  static constexpr int kVecs = kProjChunk / (kProjThreads * (16 / (int)sizeof(typename DT_<DT>::S)));
+  static constexpr int kAfterTicket = 2 * kVecs + (MODE == kProjSumsq ? 0 : kVecs);
+};
 
 // One chunk of a projection launch: the chunk's elements read (theta and
 // theta0), updated and written back, and for the SUMSQ modes the chunk's
@@ -924,10 +1088,8 @@ __device__ __forceinline__ void proj_chunk(const DzChunk& ch, float alpha, doubl
   char* tp = (char*)ch.ptr;
   const char* ap = (const char*)ch.aux;
   double acc = 0.0;
-  const bool aligned = (ch.meta & kDzMetaAligned) != 0u;
-  if (ch.n == (uint32_t)kProjChunk && aligned) {
-    constexpr int kPer = 16 / kES;  // elements per 16-byte vector
-    constexpr int kVecsPerThread = kProjChunk / (kProjThreads * kPer);
+  if (proj_full_chunk(ch)) {
+    constexpr int kVecsPerThread = ProjChunkOps<DT, MODE>::kVecs;
     // alpha in both 16-bit lanes (the ZO modes' alpha is a value of T)
     const uint32_t alpha2 = (kES == 2 && MODE != kProjApplyF32) ? DT_<DT>::from_f(alpha) * 0x10001u : 0u;
     dz_u32x4 vt[kVecsPerThread], va[kVecsPerThread];
@@ -1040,7 +1202,7 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
     bool have_desc = false;
     if ((rfl_u32(threadIdx.x) >> 6) == 0) {  // wave 0 (uniform branch)
       const uint32_t cd = rfl_u32(sidx[(k + 2) % 4]);
-      if (threadIdx.x == 0) grabbed = atomicAdd(mine, 1u);
+      if (threadIdx.x == 0) grabbed = ticket_take(mine);
       if (cd < nchunks) {
         const DzChunk* src = chunks + cd;
         n_ptr = src->ptr;
@@ -1050,7 +1212,17 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
         have_desc = true;
       }
     }
-    proj_chunk<DT, MODE>(ch, alpha, partials + c, red);
+    // lane 0 waits for its ticket behind the chunk's loads and stores (a full
+    // chunk issues at least kAfterTicket of them after the ticket; the
+    // partial path waits for everything), and the barrier that ends the chunk
+    // waits for LDS alone
+    if (proj_full_chunk(ch)) {
+      proj_chunk<DT, MODE>(ch, alpha, partials + c, red);
+      if (threadIdx.x == 0) ticket_wait<ProjChunkOps<DT, MODE>::kAfterTicket>();
+    } else {
+      proj_chunk<DT, MODE>(ch, alpha, partials + c, red);
+      if (threadIdx.x == 0) ticket_wait<0>();
+    }
     if (threadIdx.x == 0) {
       sidx[(k + 3) % 4] = (uint32_t)min((uint64_t)grabbed * ncnt + j, nch);
       if (have_desc) {
@@ -1062,7 +1234,7 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
         d.meta = n_meta;
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   if (threadIdx.x == 0) {
     const uint32_t done = atomicAdd(counters + kDoneSlot * kCounterStride, 1u);

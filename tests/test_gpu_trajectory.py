@@ -344,7 +344,7 @@ def test_c4_fifty_steps_with_a_dizo_event_bit_exact(capsys):
 def test_c5_two_whole_steps_bit_exact():
     """Config C5 (OPT-30B bf16, 771 tensors, 29.6 G elements, batch 8 x 2 x
     256, unpadded): two whole ZO steps of the library trainer, forwards
-    included (its three-way pass on the wave-slice loop), against the
+    included (its three-way pass on the prefetching tile loop), against the
     reference's expressions in the recipe form fed the exported z, one tensor
     at a time (three 59 GB copies of the model fit; a fourth would not): the
     losses and every weight bit for bit."""
