@@ -50,6 +50,7 @@ SIGNATURES = {
     "dz_table_matches": (_i32, [_p, _p, _i32]),
     "dz_table_z_offset": (_i32, [_p, _i32, C.POINTER(_u64)]),
     "dz_table_time_next": (_i32, [_p, _p, _p]),
+    "dz_table_set_prefetch_min_tiles": (_i32, [_p, _u32]),
     "dz_perturb": (_i32, [_p, _u64, _f32, _f32, _p, _p]),
     "dz_update": (_i32, [_p, _u64, _f32, _f32, _p, _p, _p, _p]),
     "dz_restore_update": (_i32, [_p, _u64, _f32, _f32, _f32, _p, _p, _p, _p]),

@@ -232,6 +232,9 @@ struct dz_table {
   uint32_t* d_counters = nullptr;  // work counters of the persistent RMW / projection kernels
   DeviceState* dev = nullptr;
   dz::LaunchEvents timing;  // dz_table_time_next's request for the next launching call
+  // launches of at least this many tiles run the prefetching tile loop (where
+  // the mode allows it; dz_table_set_prefetch_min_tiles)
+  uint32_t prefetch_min_tiles = DZ_RMW_PREFETCH_MIN_TILES;
 };
 
 namespace {
@@ -318,7 +321,8 @@ int32_t rmw(dz_table* t, int mode, const dz::DzScalars& s, const dz::DzScalarPtr
   }
   if (ntiles == 0) return record_unlaunched(ev, stream);
   hipError_t e = dz::launch_rmw(t->dtype, mode, chunks, ntiles, nfull, rmw_grid(t, mode, ntiles),
-                                t->dev->tab[t->dtype], s, p, t->d_counters, (hipStream_t)stream, ev);
+                                t->dev->tab[t->dtype], s, p, t->d_counters, ntiles >= t->prefetch_min_tiles,
+                                (hipStream_t)stream, ev);
   if (e != hipSuccess) return hip_fail(e, "rmw kernel launch");
   return DZ_OK;
 }
@@ -596,6 +600,13 @@ int32_t dz_table_z_offset(const dz_table* t, int32_t idx, uint64_t* out) {
   if (!t || !out) return fail(DZ_ERR_INVALID, "NULL argument");
   if (idx < 0 || idx >= t->n) return fail(DZ_ERR_INVALID, "tensor index out of range");
   *out = t->zoff[idx];
+  return DZ_OK;
+}
+
+int32_t dz_table_set_prefetch_min_tiles(dz_table* t, uint32_t min_tiles) {
+  int32_t rc = check_table(t);
+  if (rc) return rc;
+  t->prefetch_min_tiles = min_tiles;
   return DZ_OK;
 }
 

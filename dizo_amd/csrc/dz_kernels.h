@@ -96,12 +96,23 @@ __host__ __device__ constexpr int rmw_lds_table_bytes(int dtype, int mode) {
 //     three-way pass (OPT-30B 22.9 against 24.0 ms); every streaming pass
 //     runs slower with it (OPT-13B fp16 perturb 7.92 against 7.71 ms,
 //     OPT-125m fp32 0.149 against 0.125 ms). Now off by default.
-// Both can be set per mode with -D; the slice loop takes precedence.
+//   DZ_RMW_PREFETCH_MIN_TILES: a table's default for the launches that use the
+//     prefetching loop: those of at least this many tiles
+//     (dz_table_set_prefetch_min_tiles sets it per table). In the ZO step, after the
+//     forwards, a short three-way pass streams at the one-block passes'
+//     rate on the plain loop, and only a long one runs at the lowered clock
+//     whose ALU time the prefetching loop overlaps: OPT-2.7B fp16 (77 K
+//     tiles) 1.556 ms plain against 1.63 ms prefetching, OPT-13B fp16 (384 K
+//     tiles) 8.19-8.21 against 7.97-8.00 ms (same box, alternating builds).
+// Both masks can be set per mode with -D; the slice loop takes precedence.
 #ifndef DZ_RMW_PREFETCH_MASK
 #define DZ_RMW_PREFETCH_MASK ((1 << (4 * 1 + 3)) | (1 << (4 * 2 + 3)))
 #endif
 #ifndef DZ_RMW_SLICE_MASK
 #define DZ_RMW_SLICE_MASK 0
+#endif
+#ifndef DZ_RMW_PREFETCH_MIN_TILES
+#define DZ_RMW_PREFETCH_MIN_TILES 160000
 #endif
 constexpr int kCounters = DZ_RMW_COUNTERS;
 constexpr int kSliceCounters = 16;
@@ -155,10 +166,11 @@ struct LaunchEvents {
 };
 
 // The first nfull chunks are full, aligned tiles; the rest are partial or
-// misaligned.
+// misaligned. prefetch: run the prefetching tile loop where the mode allows
+// it (DZ_RMW_PREFETCH_MASK); the caller sets it for long launches.
 hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t nfull, uint32_t grid,
                       const void* qtab, const DzScalars& s, const DzScalarPtrs& p, uint32_t* counters,
-                      hipStream_t st, const LaunchEvents& ev = {});
+                      bool prefetch, hipStream_t st, const LaunchEvents& ev = {});
 // Persistent: `grid` workgroups share the chunks through `counters` (zero
 // before the launch; the launch leaves them at zero).
 hipError_t launch_proj(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t ngroups,

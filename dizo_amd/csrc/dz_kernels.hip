@@ -894,7 +894,9 @@ __device__ __forceinline__ uint32_t rmw_tiles_prefetch(const DzChunk* __restrict
   return k;
 }
 
-template <int DT, int MODE>
+// kPF: run the prefetching tile loop over the workgroup's leading full tiles
+// (only where RmwTraits::kPrefetch allows it; the launcher picks it by size).
+template <int DT, int MODE, bool kPF>
 __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU)) rmw_kernel(const DzChunk* __restrict__ chunks,
                                                           uint32_t nchunks, uint32_t nfull,
                                                           const void* __restrict__ qtab,
@@ -945,7 +947,7 @@ __global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU
     store_table<DT, MODE>(tab, qs, sc);
     __syncthreads();
     uint32_t k0 = 0;
-    if constexpr (Tr::kPrefetch) k0 = rmw_tiles_prefetch<DT, MODE>(chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j, qtab);
+    if constexpr (Tr::kPrefetch && kPF) k0 = rmw_tiles_prefetch<DT, MODE>(chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j, qtab);
     rmw_tiles<DT, MODE>(k0, chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j);
   }
   if (threadIdx.x == 0) {
@@ -1376,23 +1378,29 @@ __global__ void __launch_bounds__(256) philox_kernel(uint64_t seed, uint32_t str
 template <int DT>
 static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t nfull, uint32_t grid,
                                 const void* tab, const DzScalars& s, const DzScalarPtrs& p,
-                                uint32_t* counters, hipStream_t st, const LaunchEvents& ev) {
+                                uint32_t* counters, bool prefetch, hipStream_t st, const LaunchEvents& ev) {
   switch (mode) {
     case kModePerturb:
-      DZ_LAUNCH((rmw_kernel<DT, kModePerturb>), dim3(grid), dim3(kRmwThreads), st, ev,
+      DZ_LAUNCH((rmw_kernel<DT, kModePerturb, false>), dim3(grid), dim3(kRmwThreads), st, ev,
                          chunks, nchunks, nfull, tab, s, p, counters);
       break;
     case kModeUpdate:
-      DZ_LAUNCH((rmw_kernel<DT, kModeUpdate>), dim3(grid), dim3(kRmwThreads), st, ev,
+      DZ_LAUNCH((rmw_kernel<DT, kModeUpdate, false>), dim3(grid), dim3(kRmwThreads), st, ev,
                          chunks, nchunks, nfull, tab, s, p, counters);
       break;
     case kModeRestoreUpdate:
-      DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdate>), dim3(grid), dim3(kRmwThreads),
+      DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdate, false>), dim3(grid), dim3(kRmwThreads),
                          st, ev, chunks, nchunks, nfull, tab, s, p, counters);
       break;
     case kModeRestoreUpdatePerturb:
-      DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdatePerturb>), dim3(grid), dim3(kRmwThreads),
-                         st, ev, chunks, nchunks, nfull, tab, s, p, counters);
+      // the caller asks for the prefetching loop on long launches (DZ_RMW_PREFETCH_MIN_TILES)
+      if (RmwTraits<DT, kModeRestoreUpdatePerturb>::kPrefetch && prefetch) {
+        DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdatePerturb, true>), dim3(grid), dim3(kRmwThreads),
+                           st, ev, chunks, nchunks, nfull, tab, s, p, counters);
+      } else {
+        DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdatePerturb, false>), dim3(grid), dim3(kRmwThreads),
+                           st, ev, chunks, nchunks, nfull, tab, s, p, counters);
+      }
       break;
     default:
       return hipErrorInvalidValue;
@@ -1402,11 +1410,14 @@ static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunk
 
 hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t nfull, uint32_t grid,
                       const void* tab, const DzScalars& s, const DzScalarPtrs& p, uint32_t* counters,
-                      hipStream_t st, const LaunchEvents& ev) {
+                      bool prefetch, hipStream_t st, const LaunchEvents& ev) {
   switch (dtype) {
-    case DZ_F32: return launch_rmw_dt<DZ_F32>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, st, ev);
-    case DZ_F16: return launch_rmw_dt<DZ_F16>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, st, ev);
-    case DZ_BF16: return launch_rmw_dt<DZ_BF16>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, st, ev);
+    case DZ_F32:
+      return launch_rmw_dt<DZ_F32>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, prefetch, st, ev);
+    case DZ_F16:
+      return launch_rmw_dt<DZ_F16>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, prefetch, st, ev);
+    case DZ_BF16:
+      return launch_rmw_dt<DZ_BF16>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, prefetch, st, ev);
     default: return hipErrorInvalidValue;
   }
 }

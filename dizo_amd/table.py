@@ -103,6 +103,12 @@ class _Table:
             raise DzError(f"{self.what}: a registered tensor's storage moved since the table was "
                           "built (rebuild the table)")
 
+    def set_prefetch_min_tiles(self, min_tiles: int) -> None:
+        """Launches of the fused restore+update+next perturb pass with at least
+        min_tiles tiles run the prefetching tile loop (16-bit tables; 0: every
+        launch). The computed values do not depend on it."""
+        L.call("dz_table_set_prefetch_min_tiles", self.handle, int(min_tiles))
+
     def time_next(self, start: "torch.cuda.Event | None", stop: "torch.cuda.Event | None") -> None:
         """The next launching call on this table records `start` as its first
         kernel starts and `stop` as its last kernel ends (either may be None).

@@ -43,6 +43,17 @@ def _make_tensors(dt, seed, sizes=SIZES, misaligned=(3, 6)):
     return tensors, host, keep
 
 
+def _fused_table(tensors, prefetch, **kw):
+    """A ZO table whose restore+update+next perturb launches run the
+    prefetching tile loop at any size (prefetch=True) or the size rule's
+    choice (prefetch=False: the plain loop for these small tables)."""
+    from dizo_amd.table import ZOTable
+    tab = ZOTable(tensors, **kw)
+    if prefetch:
+        tab.set_prefetch_min_tiles(0)
+    return tab
+
+
 def _z_host(table, seed, dt):
     return [rng.tensor_z_bits(seed, off, n, dt) for off, n in zip(table.z_offsets, table.numels)]
 
@@ -128,13 +139,15 @@ def test_full_step_sequence_matches_oracle(dt):
 
 
 @pytest.mark.parametrize("dt", DTS)
-def test_restore_update_perturb_matches_oracle(dt):
+@pytest.mark.parametrize("prefetch", [False, True])
+def test_restore_update_perturb_matches_oracle(dt, prefetch):
     """Restore + update of step seed, then +1 of step next_seed, in one pass: the
-    same bits as the three passes, and as the oracle."""
+    same bits as the three passes, and as the oracle (plain and prefetching
+    tile loops)."""
     from dizo_amd.table import ZOTable
     tensors, host, keep = _make_tensors(dt, 61)
     clones = [t.clone() for t in tensors]
-    tab = ZOTable(tensors)
+    tab = _fused_table(tensors, prefetch)
     seed, nxt, eps, g, lr = 9090, 9091, 1e-3, 0.6875, 9.9e-07
     tab.restore_update_perturb(seed, nxt, eps, g, lr)
     z1, z2 = _z_host(tab, seed, dt), _z_host(tab, nxt, dt)
@@ -203,20 +216,21 @@ def _opt_like_sizes(target_elems: int, d: int = 768):
 
 @pytest.mark.parametrize("dt", DTS)
 @pytest.mark.parametrize("target", [200_000, 1_200_000, 6_000_000, 90_000_000])
-def test_multi_tile_launches_match_torch(dt, target):
+@pytest.mark.parametrize("prefetch", [False, True])
+def test_multi_tile_launches_match_torch(dt, target, prefetch):
     """Tables of 3 to ~1400 tiles (grids below and above the counter fan-out,
     several tiles per workgroup): every element is processed exactly once per
     launch, also on consecutive launches (the work counters reset themselves).
     Checked against the reference's expressions run by ROCm torch with the
-    exported z."""
-    from dizo_amd.table import ZOTable
+    exported z; the fused three-way pass on the plain and the prefetching
+    tile loop."""
     dev = torch.device("cuda", 0)
     sizes = _opt_like_sizes(target, d=64 if target < 1_000_000 else 768)
-    print(f"dt={dt} target={target} tensors={len(sizes)} elems={sum(sizes)}", flush=True)
+    print(f"dt={dt} target={target} prefetch={prefetch} tensors={len(sizes)} elems={sum(sizes)}", flush=True)
     gen = torch.Generator(device=dev).manual_seed(target)
     tensors = [(torch.randn(n, device=dev, generator=gen) * 0.02).to(DT_TORCH[dt]) for n in sizes]
     ref = [t.clone() for t in tensors]
-    tab = ZOTable(tensors)
+    tab = _fused_table(tensors, prefetch)
     seed, eps, g, lr = 1000 + target % 977, 1e-3, -2.25, 1e-6
     zs = [tab.export_z(seed, i) for i in range(len(tensors))]
     for s_ in (1, -2):
@@ -360,16 +374,16 @@ def test_update_rounds_ties_like_torch_cpu_and_cuda():
     assert body == 0
 
 
-def test_single_tensor_beyond_2_32_elements():
+@pytest.mark.parametrize("prefetch", [False, True])
+def test_single_tensor_beyond_2_32_elements(prefetch):
     """One fp16 tensor of 2^32 + 8200 elements (8.6 GB), its z offset past 2^32
-    as well: perturb and the fused restore+update+perturb, checked against the
-    oracle on windows at the start, across the 2^32 element boundary and at the
-    ragged end."""
-    from dizo_amd.table import ZOTable
+    as well: perturb and the fused restore+update+perturb (plain and
+    prefetching tile loops), checked against the oracle on windows at the
+    start, across the 2^32 element boundary and at the ragged end."""
     n = (1 << 32) + 8200
     t = torch.zeros(n, dtype=torch.float16, device="cuda")
     off = 3 << 31  # the tensor's first z index
-    tab = ZOTable([t], z_offsets=[off])
+    tab = _fused_table([t], prefetch, z_offsets=[off])
     seed, eps, g, lr = 99, 1e-3, -1.25, 1e-6
     tab.perturb(seed, 1.0, eps)
     tab.restore_update_perturb(seed, seed + 1, eps, g, lr)
@@ -386,13 +400,14 @@ def test_single_tensor_beyond_2_32_elements():
 
 
 @pytest.mark.parametrize("dt", DTS)
-def test_tiles_across_the_2_32_counter_boundary(dt):
+@pytest.mark.parametrize("prefetch", [False, True])
+def test_tiles_across_the_2_32_counter_boundary(dt, prefetch):
     """Philox counters q = e >> 3 past 2^32: z offsets put one tile of each tile
     size across q = 2^32 (its counters' high word changes inside the tile),
     the tiles before it at high word 0 and the tiles after it at high word 1.
-    Every mode (perturb, update, restore+update, restore+update+next perturb),
-    every element against the oracle."""
-    from dizo_amd.table import ZOTable
+    Every mode (perturb, update, restore+update, restore+update+next perturb;
+    the last on the plain and the prefetching tile loop, which hands a tile
+    across the boundary to the plain loop), every element against the oracle."""
     sizes = [200_000, 70_001]
     # the first tensor starts 5000 groups below q = 2^32; the second 904 groups
     # below q = 2^33, so its first tile crosses at once
@@ -400,7 +415,7 @@ def test_tiles_across_the_2_32_counter_boundary(dt):
     host = [random_theta(n, dt, 40 + i) for i, n in enumerate(sizes)]
     dev = torch.device("cuda", 0)
     tensors = [to_torch(b, dt, dev) for b in host]
-    tab = ZOTable(tensors, z_offsets=offs)
+    tab = _fused_table(tensors, prefetch, z_offsets=offs)
     seed, seed2, eps, g, lr = 512, 513, 1e-3, 0.75, 1e-3
     z1 = [rng.tensor_z_bits(seed, o, n, dt) for o, n in zip(offs, sizes)]
     z2 = [rng.tensor_z_bits(seed2, o, n, dt) for o, n in zip(offs, sizes)]
@@ -428,13 +443,14 @@ def test_tiles_across_the_2_32_counter_boundary(dt):
 
 
 @pytest.mark.parametrize("dt", DTS)
-def test_special_values_follow_ieee_like_the_oracle(dt):
+@pytest.mark.parametrize("prefetch", [False, True])
+def test_special_values_follow_ieee_like_the_oracle(dt, prefetch):
     """theta holding +-inf, NaN, +-0, the largest finite value and the smallest
     subnormal, among ordinary values: every RMW mode, then the projection's
     apply and reverse with a supplied alpha, against the oracle (NaN equal to
     NaN, as torch's expressions give NaN there too)."""
     from dizo_amd._lib import DZ_PROJ_APPLY, DZ_PROJ_REVERSE
-    from dizo_amd.table import ProjTable, ZOTable
+    from dizo_amd.table import ProjTable
     big = {F16: 65504.0, BF16: 3.3895314e38, F32: 3.4028235e38}[dt]
     tiny = {F16: 5.96e-8, BF16: 9.2e-41, F32: 1.4e-45}[dt]
     specials = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, big, -big, tiny, -tiny], dtype=np.float32)
@@ -444,7 +460,7 @@ def test_special_values_follow_ieee_like_the_oracle(dt):
     h0 = A.from_f32(x, dt)
     dev = torch.device("cuda", 0)
     t = to_torch(h0, dt, dev)
-    tab = ZOTable([t])
+    tab = _fused_table([t], prefetch)
     seed, seed2, eps, g, lr = 77, 78, 1e-3, 2.5, 1e-3
     z = rng.tensor_z_bits(seed, 0, n, dt)
     z2 = rng.tensor_z_bits(seed2, 0, n, dt)
