@@ -685,7 +685,10 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, uint32_t first, u
 // chunk list holds its nfull full, aligned tiles first. The last workgroup to
 // finish resets the counters for the next launch.
 //
-// Wave-level loop (RmwTraits::kSlices): each wave takes slices of 64 * G
+// Three loops, chosen per mode at compile time (DZ_RMW_SLICE_MASK,
+// DZ_RMW_PREFETCH_MASK) and, for the prefetching one, per launch by size:
+//
+// Wave-level loop (RmwTraits::kSlices; off by default): each wave takes slices of 64 * G
 // groups (a sixteenth of a tile; slice id = ticket * K + j from counter j of
 // the K = 16 slice counters, wave w of every workgroup using counter w mod K,
 // so every counter serves waves on every XCD) and loads, computes and stores
@@ -694,11 +697,17 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, uint32_t first, u
 // tile, all 16 waves of a workgroup load, wait, compute and store in step,
 // and a tile's load latency and its compute add up instead of overlapping.
 //
-// Workgroup-level loop (the other launches): the workgroup takes whole
-// tiles from counters j of K = min(8, grid / 8), workgroup b using counter
-// (b / 8) mod K; wave 0 keeps a ring in LDS (while tile k streams, the index
-// of tile k+3 is taken and the descriptor of tile k+2 is loaded) and a
-// barrier ends each tile.
+// Workgroup-level loop (rmw_tiles): the workgroup takes whole tiles from
+// counters j of K = min(8, grid / 8), workgroup b using counter (b / 8) mod
+// K; wave 0 keeps a ring in LDS (while tile k streams, the index of tile k+3
+// is taken and the descriptor of tile k+2 is loaded) and a barrier ends each
+// tile.
+//
+// Prefetching workgroup-level loop (rmw_tiles_prefetch, the 16-bit
+// restore+update+next perturb passes of long launches): the same tiles and
+// ring, with the next full tile's loads issued before each tile's work; it
+// hands the workgroup's remaining tiles to rmw_tiles at its first tile that
+// is not full.
 // ---------------------------------------------------------------------------
 template <int DT, int MODE>
 __device__ __forceinline__ void rmw_slice(const DzChunk& ch, uint32_t c, uint32_t nfull, uint32_t first,
