@@ -111,6 +111,11 @@ __host__ __device__ constexpr int rmw_lds_table_bytes(int dtype, int mode) {
 #ifndef DZ_RMW_SLICE_MASK
 #define DZ_RMW_SLICE_MASK 0
 #endif
+// The bf16 reverse pass's quotient by one multiply with fp32(1 / alpha) (0:
+// the IEEE division for every element; the values are the same).
+#ifndef DZ_PROJ_RECIP_DIV
+#define DZ_PROJ_RECIP_DIV 1
+#endif
 #ifndef DZ_RMW_PREFETCH_MIN_TILES
 #define DZ_RMW_PREFETCH_MIN_TILES 160000
 #endif

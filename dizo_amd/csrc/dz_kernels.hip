@@ -1037,13 +1037,34 @@ __device__ __forceinline__ void acc_sq_pair(uint32_t d, double* acc) {
   *acc += d1 * d1;
 }
 
+// REVERSE's quotient R_T(fp32(d) / alpha) for bf16 T. The reference's fp32
+// division rounded to bf16 equals bf16(d * inv), inv = fp32(1 / alpha), for
+// every pair of bf16 values d, alpha with inv finite, unless the product is
+// nonzero and below the smallest normal fp32 value: checked over all 2^32
+// pairs (RN_bf16 of the fp32 quotient is RN_bf16 of the exact quotient, since
+// fp32 carries 24 >= 2 * 8 + 2 bits, and for normal operands a bf16 quotient
+// is at least 2^-16 of itself away from a bf16 rounding midpoint, where the
+// product's error is under 2^-23). Elements outside that range divide. One
+// multiply replaces the IEEE division sequence per element.
+struct RecipDiv {
+  float inv;  // fp32(1 / alpha)
+  bool ok;    // inv is finite (alpha is neither 0, infinite nor below 2^-128)
+};
+__device__ __forceinline__ RecipDiv recip_div(float alpha) {
+  const float inv = 1.0f / alpha;
+  return RecipDiv{inv, __builtin_isfinite(inv) != 0};
+}
+__device__ __forceinline__ bool recip_quotient_ok(float q) {
+  return !(q != 0.0f && __builtin_fabsf(q) < 0x1p-126f);  // NaN, zero and normal quotients
+}
+
 // proj_elem for the two 16-bit elements of a word, in packed arithmetic where
 // the reference's op has both operands in T (SUMSQ, APPLY and the subtract /
 // add of REVERSE); alpha2 holds alpha in both lanes. APPLY_F32 is not here
 // (its fp32 alpha keeps v and the sum in fp32).
 template <int DT, int MODE>
 __device__ __forceinline__ uint32_t proj_word16(uint32_t th, uint32_t t0, uint32_t alpha2, float alpha,
-                                                double* acc) {
+                                                const RecipDiv& rd, double* acc) {
   const uint32_t d = sub_pair<DT>(th, t0);
   if constexpr (MODE == kProjSumsq) {
     acc_sq_pair<DT>(d, acc);
@@ -1052,6 +1073,14 @@ __device__ __forceinline__ uint32_t proj_word16(uint32_t th, uint32_t t0, uint32
     uint32_t v;
     if constexpr (MODE == kProjApply) {
       v = mul_pair<DT>(d, alpha2);
+    } else if constexpr (DT == DZ_BF16) {
+      const float x0 = bf16_lo_f(d), x1 = bf16_hi_f(d);
+      float v0 = x0 * rd.inv, v1 = x1 * rd.inv;
+      if (!(rd.ok && recip_quotient_ok(v0) && recip_quotient_ok(v1))) {
+        v0 = x0 / alpha;
+        v1 = x1 / alpha;
+      }
+      v = pack_bf16(v0, v1);
     } else {
       const float v0 = DT_<DT>::to_f(d & 0xffffu) / alpha;
       const float v1 = DT_<DT>::to_f(d >> 16) / alpha;
@@ -1103,6 +1132,9 @@ __device__ __forceinline__ void proj_chunk(const DzChunk& ch, float alpha, doubl
     constexpr int kVecsPerThread = ProjChunkOps<DT, MODE>::kVecs;
     // alpha in both 16-bit lanes (the ZO modes' alpha is a value of T)
     const uint32_t alpha2 = (kES == 2 && MODE != kProjApplyF32) ? DT_<DT>::from_f(alpha) * 0x10001u : 0u;
+    const RecipDiv rd = (DZ_PROJ_RECIP_DIV && DT == DZ_BF16 && (MODE == kProjReverse || MODE == kProjReverseSumsq))
+                            ? recip_div(alpha)
+                            : RecipDiv{0.0f, false};
     dz_u32x4 vt[kVecsPerThread], va[kVecsPerThread];
 #pragma unroll
     for (int u = 0; u < kVecsPerThread; ++u) {
@@ -1116,7 +1148,7 @@ __device__ __forceinline__ void proj_chunk(const DzChunk& ch, float alpha, doubl
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if constexpr (kES == 2 && MODE != kProjApplyF32) {
-          o[i] = proj_word16<DT, MODE>(vt[u][i], va[u][i], alpha2, alpha, &acc);
+          o[i] = proj_word16<DT, MODE>(vt[u][i], va[u][i], alpha2, alpha, rd, &acc);
         } else if constexpr (kES == 2) {
           uint32_t r0, r1;
           proj_elem<DT>(MODE, vt[u][i] & 0xffffu, va[u][i] & 0xffffu, alpha, &r0, &acc);

@@ -222,3 +222,56 @@ def test_more_groups_than_the_lds_alpha_table(dt):
     for g in range(0, G, 97):
         assert s[g] == pytest.approx(A.group_sumsq(rev[g], t0_all[g * n:(g + 1) * n], dt), rel=1e-12), g
     tab.close()
+
+
+def _edge_alphas(dt):
+    """Alphas across the range: subnormal ones (for bf16, 1 / alpha overflows
+    below 2^-128), the smallest normal, tiny, typical, huge and negative
+    values, and random ratios near 1."""
+    r = np.random.default_rng(17)
+    vals = [2.0 ** -126, 2.0 ** -100, 2.0 ** -64, 1e-8, 1e-3, 0.5, 0.9, 1.0, 1.1, 2.0, 3.0, 7.0, 1e3, 2.0 ** 60,
+            -0.75, -3.0] + list(r.uniform(0.5, 2.0, 16))
+    bits = [int(b) for b in from_f32(np.array(vals, dtype=np.float32), dt)]
+    if dt == BF16:
+        bits += [0x0001, 0x0040, 0x007f, 0x0080, 0x7f7f]  # subnormals, min normal, max
+    else:
+        bits += [0x0001, 0x0200, 0x03ff, 0x0400, 0x7bff]
+    out = []
+    for b in bits:
+        v = float(to_f32(np.array([b], dtype=A.BITS_DTYPE[dt]), dt)[0])
+        if v != 0 and np.isfinite(v) and b not in out:
+            out.append(b)
+    return np.array(out, dtype=A.BITS_DTYPE[dt])
+
+
+@pytest.mark.parametrize("dt", [BF16, F16])
+def test_reverse_every_dividend_matches_oracle(dt):
+    """reverse and reverse+norm with theta0 = 0 and theta running through all
+    65536 16-bit patterns (inf, NaN, subnormals and zeros included), so the
+    quotient R_T(R_T(theta - theta0) / alpha) meets every dividend, for ~40
+    alphas from subnormal to huge: bit for bit against the oracle's IEEE
+    division (the bf16 kernel divides by multiplying with fp32(1 / alpha),
+    falling back to the division where that could round differently)."""
+    from dizo_amd._lib import DZ_PROJ_REVERSE, DZ_PROJ_REVERSE_SUMSQ
+    from dizo_amd.table import ProjTable
+    dev = torch.device("cuda", 0)
+    alphas = _edge_alphas(dt)
+    G = len(alphas)
+    every = np.arange(65536, dtype=np.uint32).astype(A.BITS_DTYPE[dt])
+    zeros = np.zeros(65536, dtype=A.BITS_DTYPE[dt])
+    ths = [to_torch(every, dt, dev) for _ in range(G)]
+    t0s = [to_torch(zeros, dt, dev) for _ in range(G)]
+    tab = ProjTable(ths, t0s)
+    alpha_t = to_torch(alphas, dt, dev)
+    for mode, what in ((DZ_PROJ_REVERSE, "reverse"), (DZ_PROJ_REVERSE_SUMSQ, "reverse+norm")):
+        for t in ths:
+            t.copy_(to_torch(every, dt, dev))
+        if mode == DZ_PROJ_REVERSE_SUMSQ:
+            sumsq = torch.empty(G, dtype=torch.float64, device=dev)
+            tab.project(alpha_t, mode, sumsq=sumsq)
+        else:
+            tab.project(alpha_t, mode)
+        for g in range(G):
+            want = A.reverse(every, zeros, alphas[g:g + 1], dt)
+            assert_bits_equal(to_bits(ths[g]), want, dt, f"{what}, alpha bits {hex(int(alphas[g]))}")
+    tab.close()
