@@ -84,13 +84,13 @@ __host__ __device__ constexpr int rmw_lds_table_bytes(int dtype, int mode) {
 // Tile loops of the RMW launches, by bit 4 * dtype + mode (dtype DZ_F32 0,
 // DZ_F16 1, DZ_BF16 2; mode as RmwMode):
 //   DZ_RMW_PREFETCH_MASK: the workgroup-level loop that loads the next full
-//     tile while it computes the current one (rmw_tiles_prefetch). Measured
-//     on the MI355X, same box, alternating builds: the restore+update+next
-//     perturb passes, whose ALU work per tile is the largest, gain (OPT-13B
-//     fp16 8.15-8.18 -> 7.97 ms, OPT-30B bf16 22.5-23.0 -> 20.4-20.6 ms);
-//     every single-Philox pass loses (OPT-13B fp16 perturb 7.66 -> 8.86 ms,
-//     OPT-30B bf16 17.8 -> 21.0 ms), and so does the fp32 three-way pass
-//     (OPT-125m 0.121 -> 0.126 ms), so those keep the plain loop.
+//     tile during the current one (rmw_tiles_prefetch; the loads go out
+//     half-way through the tile's work). Measured on the MI355X, same box,
+//     alternating builds: the restore+update+next perturb passes, whose ALU
+//     work per tile is the largest, gain (OPT-13B fp16 7.86-7.90 -> 7.58-7.61
+//     ms, OPT-30B bf16 20.10-20.16 -> 19.83-19.95 ms); the single-Philox
+//     passes run the same either way (OPT-13B fp16 perturb 7.66-7.69 ms both,
+//     OPT-30B bf16 17.76 ms both), so they keep the plain loop.
 //   DZ_RMW_SLICE_MASK: the wave-level loop (rmw_slices), no barrier between
 //     slices. Before the prefetching loop it was the faster form of the bf16
 //     three-way pass (OPT-30B 22.9 against 24.0 ms); every streaming pass
@@ -98,12 +98,10 @@ __host__ __device__ constexpr int rmw_lds_table_bytes(int dtype, int mode) {
 //     OPT-125m fp32 0.149 against 0.125 ms). Now off by default.
 //   DZ_RMW_PREFETCH_MIN_TILES: a table's default for the launches that use the
 //     prefetching loop: those of at least this many tiles
-//     (dz_table_set_prefetch_min_tiles sets it per table). In the ZO step, after the
-//     forwards, a short three-way pass streams at the one-block passes'
-//     rate on the plain loop, and only a long one runs at the lowered clock
-//     whose ALU time the prefetching loop overlaps: OPT-2.7B fp16 (77 K
-//     tiles) 1.556 ms plain against 1.63 ms prefetching, OPT-13B fp16 (384 K
-//     tiles) 8.19-8.21 against 7.97-8.00 ms (same box, alternating builds).
+//     (dz_table_set_prefetch_min_tiles sets it per table). 0: every launch of a
+//     mode in the mask. With the next tile's loads issued half-way, the
+//     prefetching loop is also the faster one for a short pass (OPT-2.7B fp16,
+//     77 K tiles, in the ZO step: 1.544-1.545 against 1.562-1.563 ms).
 // Both masks can be set per mode with -D; the slice loop takes precedence.
 #ifndef DZ_RMW_PREFETCH_MASK
 #define DZ_RMW_PREFETCH_MASK ((1 << (4 * 1 + 3)) | (1 << (4 * 2 + 3)))
@@ -117,7 +115,7 @@ __host__ __device__ constexpr int rmw_lds_table_bytes(int dtype, int mode) {
 #define DZ_PROJ_RECIP_DIV 1
 #endif
 #ifndef DZ_RMW_PREFETCH_MIN_TILES
-#define DZ_RMW_PREFETCH_MIN_TILES 160000
+#define DZ_RMW_PREFETCH_MIN_TILES 0
 #endif
 constexpr int kCounters = DZ_RMW_COUNTERS;
 constexpr int kSliceCounters = 16;

@@ -580,10 +580,28 @@ __device__ __forceinline__ void apply_store_group32(char* base, uint32_t g0, con
 // chains with the LDS lookups; with the chains in a block of their own the
 // two ran one after the other (three-way pass at OPT-13B: 8.9 -> 8.2 ms at
 // equal Philox rounds).
-template <int DT, int MODE, bool kUniformHi, int kStride>
+// kLoadNext (the prefetching tile loop): the next tile's loads, from nptr
+// into *nxt, go out once the first half of the groups are stored (for one
+// group per thread, before the Philox chains), held there by scheduling
+// barriers. Measured at OPT-13B fp16, three-way pass, same box, alternating
+// builds: 7.86-7.90 ms with the loads issued before the Philox chains,
+// 7.69-7.70 after them, 7.58-7.59 half-way, 7.60 three quarters in, and
+// 7.89 with one vector loaded after each group's store; OPT-30B bf16
+// 20.10-20.16 -> 19.83-19.89 ms half-way. Issued at the start, the next
+// tile's reads meet this tile's first stores in the memory system (rocprofv3
+// counts 18 % fewer reads in flight and 2.7 times the L2 tag stalls per
+// cycle of the perturb pass).
+template <int DT, int MODE, bool kUniformHi, int kStride, bool kLoadNext = false>
 __device__ __forceinline__ void tile_body(const DzChunk& ch, uint32_t g0, const TileRegs<DT, MODE>& r,
-                                          const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc) {
+                                          const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
+                                          uint64_t nptr = 0, TileRegs<DT, MODE>* nxt = nullptr) {
   constexpr int G = RmwTraits<DT, MODE>::kGroups;
+  // the next tile's loads go out after group kLoadAfter's stores (-1: first)
+  constexpr int kLoadAfter = G > 1 ? G / 2 - 1 : -1;
+  if constexpr (kLoadNext && kLoadAfter < 0) {
+    load_tile_at<DT, MODE, kStride>(nptr, g0, *nxt);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
   char* base = (char*)ch.ptr;
   DzU4 w[G], w2[G];
@@ -603,6 +621,13 @@ __device__ __forceinline__ void tile_body(const DzChunk& ch, uint32_t g0, const 
       o.z = combine_pair16<DT, MODE>(r.v[u].z, w[u].z, w2[u].z, lookup_pair16<DT, MODE>(w[u].z, w2[u].z, tab));
       o.w = combine_pair16<DT, MODE>(r.v[u].w, w[u].w, w2[u].w, lookup_pair16<DT, MODE>(w[u].w, w2[u].w, tab));
       st_stream(base + tile_vec_offset<DT, kStride>(g0, u), o);
+    }
+    if constexpr (kLoadNext && kLoadAfter >= 0) {
+      if (u == kLoadAfter) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile_at<DT, MODE, kStride>(nptr, g0, *nxt);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 }
@@ -705,9 +730,9 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, uint32_t first, u
 //
 // Prefetching workgroup-level loop (rmw_tiles_prefetch, the 16-bit
 // restore+update+next perturb passes of long launches): the same tiles and
-// ring, with the next full tile's loads issued before each tile's work; it
-// hands the workgroup's remaining tiles to rmw_tiles at its first tile that
-// is not full.
+// ring, with the next full tile's loads issued half-way through each
+// tile's work; it hands the workgroup's remaining tiles to rmw_tiles at its
+// first tile that is not full.
 // ---------------------------------------------------------------------------
 template <int DT, int MODE>
 __device__ __forceinline__ void rmw_slice(const DzChunk& ch, uint32_t c, uint32_t nfull, uint32_t first,
@@ -813,7 +838,7 @@ __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F7
 
 // One tile of the prefetching tile loop (see rmw_tiles_prefetch): full tile
 // k is computed from `cur` (loaded during tile k - 1) while tile k + 1 is
-// loaded into `nxt`. Returns whether tile k + 1 is a full tile (its data is
+// loaded into `nxt` (issued half-way through, tile_body). Returns whether tile k + 1 is a full tile (its data is
 // then in `nxt`); if it is not, the loads read a stand-in of the same size
 // (the quantile table), so that every path issues the same loads.
 template <int DT, int MODE>
@@ -845,9 +870,7 @@ __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk* __r
       have_desc = true;
     }
   }
-  load_tile_at<DT, MODE, kRmwThreads>(nptr, threadIdx.x, nxt);
-  __builtin_amdgcn_sched_barrier(0);
-  tile_body<DT, MODE, true, kRmwThreads>(ch, threadIdx.x, cur, tab, sc);
+  tile_body<DT, MODE, true, kRmwThreads, true>(ch, threadIdx.x, cur, tab, sc, nptr, &nxt);
   if (threadIdx.x == 0) {
     ticket_wait<2 * kVecs>();  // behind the ticket: tile k + 1's loads and tile k's stores
     sidx[(k + 3) % 4] = (uint32_t)min((uint64_t)grabbed * ncnt + j, (uint64_t)nchunks);
@@ -868,8 +891,8 @@ __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk* __r
 // over the run of full tiles a workgroup takes first (a table lists its full
 // tiles first); the rest of its tiles go through rmw_tiles. Two register
 // sets are used in turn (the loop unrolled by two, so no pending registers
-// are copied); each step is one straight block whose loads go out ahead of
-// the Philox chains; the ticket is hidden from the compiler (ticket_take); and
+// are copied); each step is one straight block whose loads go out at a fixed
+// point of it; the ticket is hidden from the compiler (ticket_take); and
 // the barrier orders LDS only. With those, the compiler's waits for a tile's
 // data count the operations behind it (the previous tile's stores and the
 // next tile's loads) instead of draining everything in flight.

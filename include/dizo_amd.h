@@ -98,11 +98,10 @@ int32_t dz_table_time_next(dz_table* t, void* start_event, void* stop_event);
  * restore+update+next perturb pass of a 16-bit table runs its prefetching
  * tile loop (the next tile loaded while the current one computes) only for
  * launches of at least min_tiles tiles; smaller launches run the plain loop.
- * The default, 160000 tiles (about 5 G elements), sits between the two
- * sizes measured on the MI355X in the ZO step: the prefetching loop is
- * slower at 77 K tiles (OPT-2.7B) and faster at 384 K (OPT-13B). 0 selects
- * it for every launch (tests use that to run it on small tables). The
- * values the passes compute do not depend on it. */
+ * The default, 0, selects it for every launch: measured on the MI355X in the
+ * ZO step it is the faster loop at 77 K tiles (OPT-2.7B) and at 384 K
+ * (OPT-13B). Tests set a large value to run the plain loop. The values the
+ * passes compute do not depend on it. */
 int32_t dz_table_set_prefetch_min_tiles(dz_table* t, uint32_t min_tiles);
 
 /* ---- ZO step (trainer.py:1429-1444, 1570-1617) -------------------------- */

@@ -44,13 +44,12 @@ def _make_tensors(dt, seed, sizes=SIZES, misaligned=(3, 6)):
 
 
 def _fused_table(tensors, prefetch, **kw):
-    """A ZO table whose restore+update+next perturb launches run the
-    prefetching tile loop at any size (prefetch=True) or the size rule's
-    choice (prefetch=False: the plain loop for these small tables)."""
+    """A ZO table whose 16-bit restore+update+next perturb launches run the
+    prefetching tile loop (prefetch=True, every launch) or the plain tile
+    loop (prefetch=False, no launch)."""
     from dizo_amd.table import ZOTable
     tab = ZOTable(tensors, **kw)
-    if prefetch:
-        tab.set_prefetch_min_tiles(0)
+    tab.set_prefetch_min_tiles(0 if prefetch else 0xFFFFFFFF)
     return tab
 
 
