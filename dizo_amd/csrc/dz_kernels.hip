@@ -729,7 +729,8 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, uint32_t first, u
 // tile.
 //
 // Prefetching workgroup-level loop (rmw_tiles_prefetch, the 16-bit
-// restore+update+next perturb passes of long launches): the same tiles and
+// restore+update+next perturb passes; a table can set a minimum launch
+// size, dz_table_set_prefetch_min_tiles): the same tiles and
 // ring, with the next full tile's loads issued half-way through each
 // tile's work; it hands the workgroup's remaining tiles to rmw_tiles at its
 // first tile that is not full.
@@ -838,9 +839,10 @@ __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F7
 
 // One tile of the prefetching tile loop (see rmw_tiles_prefetch): full tile
 // k is computed from `cur` (loaded during tile k - 1) while tile k + 1 is
-// loaded into `nxt` (issued half-way through, tile_body). Returns whether tile k + 1 is a full tile (its data is
-// then in `nxt`); if it is not, the loads read a stand-in of the same size
-// (the quantile table), so that every path issues the same loads.
+// loaded into `nxt` (the loads go out half-way through, in tile_body).
+// Returns whether tile k + 1 is a full tile (its data is then in `nxt`); if
+// it is not, the loads read a stand-in of the same size (the quantile
+// table), so that every path issues the same loads.
 template <int DT, int MODE>
 __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk* __restrict__ chunks, uint32_t nchunks,
                                                   const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
