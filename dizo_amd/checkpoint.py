@@ -47,9 +47,10 @@ from . import _lib as L
 from ._lib import DzError
 
 FORMAT = "dizo-amd-zo-journal"
-# 2: z drawn from Philox4x32-7 (version 1 journals and checkpoints were made
-# with Philox4x32-10 and do not replay on this library)
-VERSION = 2
+# 3: z drawn from Philox4x32-7 with the counter words (stream, q lo, 0, q hi).
+# Journals and checkpoints of earlier versions (version 1: Philox4x32-10;
+# version 2: counter (q lo, q hi, stream, 0)) do not replay on this library.
+VERSION = 3
 STATE_FORMAT = "dizo-amd-zo-checkpoint"
 PROJ_MODES = {"apply": L.DZ_PROJ_APPLY, "apply_f32": L.DZ_PROJ_APPLY_F32ALPHA, "reverse": L.DZ_PROJ_REVERSE}
 _DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}

@@ -206,26 +206,17 @@ static_assert(dz::kCounterWords * 4 <= kStaticOffGroupBegin, "work counters over
 
 static __device__ __align__(256) unsigned char scratch[kStaticBytes];
 
-// Tiles of one size over all of a table's tensors, in device memory.
-struct ChunkList {
-  uint32_t elems = 0;  // tile size (elements)
-  uint32_t n = 0;      // number of tiles
-  uint32_t nfull = 0;  // the first nfull tiles are full and aligned
-  DzChunk* d = nullptr;
-};
-
 struct dz_table {
   int device = -1;
   int32_t dtype = 0;
   bool projection = false;
   int32_t n = 0;
-  uint32_t chunk_elems = 0;  // tile size of the primary list (d_chunks)
+  uint32_t chunk_elems = 0;  // tile size (elements)
   uint32_t nchunks = 0;
-  uint32_t nfull = 0;        // ZO tables: the primary list's full, aligned tiles come first
+  uint32_t nfull = 0;        // ZO tables: the full, aligned tiles come first (the prefetching loop runs them)
   std::vector<uint64_t> ptrs, aux, zoff;
   std::vector<int64_t> numels;
-  std::vector<uint32_t> group_begin;  // n + 1 chunk indices (primary list)
-  ChunkList extra;                    // ZO tables: a second tile size, when launches need one
+  std::vector<uint32_t> group_begin;  // n + 1 chunk indices (projection tables)
   DzChunk* d_chunks = nullptr;
   uint32_t* d_group_begin = nullptr;
   double* d_partials = nullptr;
@@ -234,7 +225,7 @@ struct dz_table {
   dz::LaunchEvents timing;  // dz_table_time_next's request for the next launching call
   // launches of at least this many tiles run the prefetching tile loop (where
   // the mode allows it; dz_table_set_prefetch_min_tiles)
-  uint32_t prefetch_min_tiles = DZ_RMW_PREFETCH_MIN_TILES;
+  uint32_t prefetch_min_tiles = dz::kPrefetchMinTilesDefault;
 };
 
 namespace {
@@ -271,7 +262,6 @@ int32_t check_table(const dz_table* t) {
 
 void free_table(dz_table* t) {
   if (t->d_chunks) (void)hipFree(t->d_chunks);
-  if (t->extra.d) (void)hipFree(t->extra.d);
   if (t->d_group_begin) (void)hipFree(t->d_group_begin);
   if (t->d_partials) (void)hipFree(t->d_partials);
   if (t->d_counters) (void)hipFree(t->d_counters);
@@ -289,19 +279,17 @@ int32_t check_group_outputs(const dz_table* t, const double* d_sumsq, const floa
   return rc;
 }
 
-// Persistent grid of an RMW launch: DZ_RMW_NARROW_WG_PER_CU 1024-thread
-// workgroups per CU for a 64 KB delta table, one for a 128 KB table, but no
+// Persistent grid of an RMW launch: one 1024-thread workgroup per CU, but no
 // more than there are tiles.
-uint32_t rmw_grid(const dz_table* t, int mode, uint32_t ntiles) {
-  const uint32_t per_cu = dz::rmw_lds_table_bytes(t->dtype, mode) <= 65536 ? (uint32_t)DZ_RMW_NARROW_WG_PER_CU : 1u;
-  const uint32_t g = per_cu * (uint32_t)t->dev->cus;
+uint32_t rmw_grid(const dz_table* t, uint32_t ntiles) {
+  const uint32_t g = (uint32_t)t->dev->cus;
   return ntiles < g ? ntiles : g;
 }
 
-// Persistent grid of a projection launch: DZ_PROJ_WG_PER_CU workgroups per
-// CU, but no more than there are chunks.
+// Persistent grid of a projection launch: one workgroup per CU, but no more
+// than there are chunks.
 uint32_t proj_grid(const dz_table* t) {
-  const uint32_t g = (uint32_t)DZ_PROJ_WG_PER_CU * (uint32_t)t->dev->cus;
+  const uint32_t g = (uint32_t)t->dev->cus;
   return t->nchunks < g ? t->nchunks : g;
 }
 
@@ -310,19 +298,10 @@ int32_t rmw(dz_table* t, int mode, const dz::DzScalars& s, const dz::DzScalarPtr
   if (rc) return rc;
   const dz::LaunchEvents ev = take_timing(t);
   if (t->projection) return fail(DZ_ERR_INVALID, "perturb/update need a ZO table (created without anchors)");
-  const uint32_t want = (uint32_t)dz::rmw_chunk_elems(t->dtype, mode);
-  const DzChunk* chunks = t->d_chunks;
-  uint32_t ntiles = t->nchunks, nfull = t->nfull;
-  if (want != t->chunk_elems) {
-    if (want != t->extra.elems) return fail(DZ_ERR_INVALID, "internal: no tile list for this launch");
-    chunks = t->extra.d;
-    ntiles = t->extra.n;
-    nfull = t->extra.nfull;
-  }
+  const uint32_t ntiles = t->nchunks;
   if (ntiles == 0) return record_unlaunched(ev, stream);
-  hipError_t e = dz::launch_rmw(t->dtype, mode, chunks, ntiles, nfull, rmw_grid(t, mode, ntiles),
-                                t->dev->tab[t->dtype], s, p, t->d_counters, ntiles >= t->prefetch_min_tiles,
-                                (hipStream_t)stream, ev);
+  hipError_t e = dz::launch_rmw(t->dtype, mode, t->d_chunks, ntiles, rmw_grid(t, ntiles), t->dev->tab[t->dtype], s,
+                                p, t->d_counters, ntiles >= t->prefetch_min_tiles, (hipStream_t)stream, ev);
   if (e != hipSuccess) return hip_fail(e, "rmw kernel launch");
   return DZ_OK;
 }
@@ -442,8 +421,10 @@ int32_t static_scratch(int dev, StaticScratch** out) {
 
 extern "C" {
 
-// 2.0.0: z from Philox4x32-7 (1.0.0 used Philox4x32-10); dz_group_sumsq_static
-int32_t dz_version(void) { return 20000; }
+// 3.0.0: z's Philox counter words are (stream, q lo, 0, q hi) (2.0.0: (q lo,
+// q hi, stream, 0)); 2.0.0: z from Philox4x32-7 (1.0.0 used Philox4x32-10),
+// dz_group_sumsq_static
+int32_t dz_version(void) { return 30000; }
 
 const char* dz_last_error(void) { return g_last_error.c_str(); }
 
@@ -489,11 +470,7 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
   t->projection = anchor_ptrs != nullptr;
   t->n = n;
   t->dev = ds;
-  // ZO tables: the primary tile list serves the pair-table launches
-  // (restore+update), the extra list the perturb/update launches when their
-  // tile size differs.
-  t->chunk_elems = t->projection ? (uint32_t)dz::kProjChunk
-                                 : (uint32_t)dz::rmw_chunk_elems(dtype, dz::kModeRestoreUpdate);
+  t->chunk_elems = t->projection ? (uint32_t)dz::kProjChunk : (uint32_t)dz::rmw_chunk_elems(dtype);
   const int es = elem_size(dtype);
   uint64_t z = 0;
   uint64_t total_tiles = 0;
@@ -542,17 +519,6 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
   t->nchunks = (uint32_t)chunks.size();
   if (!t->projection) t->nfull = full_tiles_first(&chunks, t->chunk_elems);
   hipError_t e = upload_chunks(chunks, &t->d_chunks);
-  if (e == hipSuccess && !t->projection) {
-    const uint32_t narrow = (uint32_t)dz::rmw_chunk_elems(dtype, dz::kModePerturb);
-    if (narrow != t->chunk_elems) {
-      std::vector<DzChunk> fine;
-      build_chunks(t, narrow, &fine, nullptr);
-      t->extra.elems = narrow;
-      t->extra.n = (uint32_t)fine.size();
-      t->extra.nfull = full_tiles_first(&fine, narrow);
-      e = upload_chunks(fine, &t->extra.d);
-    }
-  }
   if (e == hipSuccess && t->projection) {
     // The finalize kernel always runs, so these exist even with no chunks.
     e = hipMalloc(&t->d_group_begin, t->group_begin.size() * sizeof(uint32_t));
@@ -770,7 +736,7 @@ int32_t dz_group_sumsq_static(const uint64_t* ptrs, const uint64_t* anchor_ptrs,
     if (e != hipSuccess) return hip_fail(e, "plan kernel launch");
   }
   if (total > 0) {
-    const uint32_t grid = std::min<uint32_t>((uint32_t)total, (uint32_t)DZ_PROJ_WG_PER_CU * (uint32_t)sc->cus);
+    const uint32_t grid = std::min<uint32_t>((uint32_t)total, (uint32_t)sc->cus);
     hipError_t e = dz::launch_proj(dtype, dz::kProjSumsq, chunks, (uint32_t)total, (uint32_t)n, grid, nullptr,
                                    partials, counters, st);
     if (e != hipSuccess) return hip_fail(e, "sumsq kernel launch");

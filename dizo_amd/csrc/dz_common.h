@@ -20,12 +20,23 @@
 //   key  = (seed mod 2^32, seed >> 32)
 //   e    = global element index (tensors laid end to end, each tensor starting
 //          at a multiple of 8, in named_parameters_to_optim order)
-//   w    = Philox4x32-7(counter = (q mod 2^32, q >> 32, stream, 0), key), q = e >> 3
+//   w    = Philox4x32-7(counter = (stream, q mod 2^32, 0, q >> 32), key), q = e >> 3
 //   h    = 16-bit field (e & 7) of w (field j = bits 16*(j&1).. of word j>>1)
 //   z    = (h & 0x8000 ? -1 : +1) * Q_T[h & 0x7fff]
 //   Q_T[i] = RNE_T( Phi^{-1}( 1/2 + (i + 1/2) / 65536 ) )
 // i.e. a sign bit and a 15-bit quantile index per element: eight normals per
 // Philox call, each already exact in the parameter dtype T.
+//
+// Counter layout. A round multiplies counter words 0 and 2 and xors words 1
+// and 3 into the products' high halves. The word that differs between the
+// lanes of a wave (q mod 2^32) sits in word 1, so it enters by an xor in
+// round 0 and is first multiplied in round 1; the stream, the zero word and
+// the high word of q (the same across a tile of one tensor) are uniform. The
+// kernels then run round 0, the products of one word in rounds 1 and 2, and
+// the xors of their results on the scalar unit: ten vector multiplies per
+// block against twelve with q in word 0. The three-way restore + update +
+// next perturbation pass draws two blocks per 8 elements, so that is four
+// fewer per group.
 #pragma once
 #include <stdint.h>
 
@@ -93,10 +104,11 @@ DZ_HD DzU4 dz_philox4x32(DzU4 c, uint32_t k0, uint32_t k1) {
     dz_mulhilo32(0xCD9E8D57u, c.z, &lo1, &hi1);
     DzU4 n;
 #if defined(__HIP_DEVICE_COMPILE__)
-    if (r == 0) {
-      // Plain xors: with a uniform counter word 1 and stream, n.x is uniform
-      // and stays on the scalar unit (the bitop3 builtin is vector-only), and
-      // so does round 1's product of it.
+    if (r < 3) {
+      // Plain xors: with the z counter layout some of these operands are
+      // uniform (all of them for n.x in round 1 and n.z in round 0), and a
+      // uniform result stays on the scalar unit, with the next round's
+      // product of it (the bitop3 builtin is vector-only).
       n.x = hi1 ^ c.y ^ k0;
       n.z = hi0 ^ c.w ^ k1;
     } else {
@@ -123,12 +135,13 @@ constexpr int kDzPhiloxRounds = 7;
 
 // The block of counter q = q_hi * 2^32 + q_lo, with the two words passed
 // apart (a caller whose q_hi is uniform across a wave keeps it scalar).
+// Counter words (stream, q_lo, 0, q_hi): see "Counter layout" above.
 DZ_HD DzU4 dz_philox_counter(uint64_t seed, uint32_t stream, uint32_t q_lo, uint32_t q_hi) {
   DzU4 c;
-  c.x = q_lo;
-  c.y = q_hi;
-  c.z = stream;
-  c.w = 0u;
+  c.x = stream;
+  c.y = q_lo;
+  c.z = 0u;
+  c.w = q_hi;
   return dz_philox4x32<kDzPhiloxRounds>(c, (uint32_t)seed, (uint32_t)(seed >> 32));
 }
 

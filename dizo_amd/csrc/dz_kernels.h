@@ -32,39 +32,20 @@ struct DzPtrArray {
 };
 
 // Read-modify-write kernel geometry. A workgroup of 1024 threads takes one
-// tile (chunk) at a time from the table's work counters; each thread owns
-// rmw_groups(dtype, mode) groups of 8 elements per tile. Measured on the
-// MI355X at OPT-13B size (643 tensors, fp16): 64 KB tiles (four groups per
-// thread) and one workgroup per CU stream best for every mode: perturb 6.4
-// TB/s against 6.05 with 16 KB tiles and two workgroups per CU (which a 64 KB
-// table would allow), restore+update 6.4-6.5 TB/s. fp32 uses 32 KB tiles (one
-// group of 8 fp32 per thread): its only workload, OPT-125m (347 MB of
-// parameters, about 40 tiles per CU), runs a pass in 126 us that way against
-// 140 us with 64 KB tiles. The macros let experiments build others.
-#ifndef DZ_RMW_GROUPS_NARROW
-#define DZ_RMW_GROUPS_NARROW 4
-#endif
-#ifndef DZ_RMW_GROUPS_WIDE16
-#define DZ_RMW_GROUPS_WIDE16 4
-#endif
-#ifndef DZ_RMW_GROUPS_WIDE32
-#define DZ_RMW_GROUPS_WIDE32 1
-#endif
-#ifndef DZ_RMW_COUNTERS
-#define DZ_RMW_COUNTERS 8
-#endif
-// Workgroups per CU for launches with a 64 KB table (the LDS would allow two).
-#ifndef DZ_RMW_NARROW_WG_PER_CU
-#define DZ_RMW_NARROW_WG_PER_CU 1
-#endif
+// tile at a time from the table's work counters; each thread owns
+// rmw_groups(dtype) groups of 8 elements per tile. Measured on the MI355X at
+// OPT-13B size (643 tensors, fp16): 64 KB tiles (four groups per thread) and
+// one workgroup per CU stream best for every mode: perturb 6.4 TB/s against
+// 6.05 with 16 KB tiles and two workgroups per CU (which a 64 KB table would
+// allow); 32 KB and 128 KB tiles were no better, and the three-way pass took
+// 7.96 ms with six groups per thread and spilled with eight. fp32 uses 32 KB
+// tiles (one group of 8 fp32 per thread): its only workload, OPT-125m (347 MB
+// of parameters, about 40 tiles per CU), runs a pass in 121 us that way
+// against 140 us with 64 KB tiles.
 constexpr int kRmwThreads = 1024;
-__host__ __device__ constexpr int rmw_groups(int dtype, int mode) {
-  return dtype == DZ_F32 ? DZ_RMW_GROUPS_WIDE32 : (rmw_pair_mode(mode) ? DZ_RMW_GROUPS_WIDE16 : DZ_RMW_GROUPS_NARROW);
-}
-// Elements per tile of an RMW launch (the table's chunk size for that launch).
-__host__ __device__ constexpr int rmw_chunk_elems(int dtype, int mode) {
-  return kRmwThreads * rmw_groups(dtype, mode) * 8;
-}
+__host__ __device__ constexpr int rmw_groups(int dtype) { return dtype == DZ_F32 ? 1 : 4; }
+// Elements per tile of an RMW launch (the table's chunk size).
+__host__ __device__ constexpr int rmw_chunk_elems(int dtype) { return kRmwThreads * rmw_groups(dtype) * 8; }
 
 // LDS bytes of the per-launch delta table of an RMW launch: 16-bit entries
 // for perturb/update of 16-bit T, 32-bit entries otherwise (fp32 deltas, or
@@ -74,69 +55,44 @@ __host__ __device__ constexpr int rmw_lds_table_bytes(int dtype, int mode) {
 }
 
 // Work counters of a table, one set per table, 128 bytes apart: kCounters
-// tile dispensers for workgroup-level loops, kSliceCounters slice
-// dispensers for the RMW kernel's wave-level loop (it hands out 16 times as
-// many work items), then (slot kDoneSlot) the number of finished
+// tile (chunk) dispensers, then (slot kDoneSlot) the number of finished
 // workgroups. Zeroed when the table is created; the last workgroup of every
 // launch puts them back to zero, so consecutive launches on one stream need
 // no reset (and no memset in a captured graph). Launches of one table must
-// not overlap in time.
-// Tile loops of the RMW launches, by bit 4 * dtype + mode (dtype DZ_F32 0,
-// DZ_F16 1, DZ_BF16 2; mode as RmwMode):
-//   DZ_RMW_PREFETCH_MASK: the workgroup-level loop that loads the next full
-//     tile during the current one (rmw_tiles_prefetch; the loads go out
-//     half-way through the tile's work). Measured on the MI355X, same box,
-//     alternating builds: the restore+update+next perturb passes, whose ALU
-//     work per tile is the largest, gain (OPT-13B fp16 7.86-7.90 -> 7.58-7.61
-//     ms, OPT-30B bf16 20.10-20.16 -> 19.83-19.95 ms); the single-Philox
-//     passes run the same either way (OPT-13B fp16 perturb 7.66-7.69 ms both,
-//     OPT-30B bf16 17.76 ms both), so they keep the plain loop.
-//   DZ_RMW_SLICE_MASK: the wave-level loop (rmw_slices), no barrier between
-//     slices. Before the prefetching loop it was the faster form of the bf16
-//     three-way pass (OPT-30B 22.9 against 24.0 ms); every streaming pass
-//     runs slower with it (OPT-13B fp16 perturb 7.92 against 7.71 ms,
-//     OPT-125m fp32 0.149 against 0.125 ms). Now off by default.
-//   DZ_RMW_PREFETCH_MIN_TILES: a table's default for the launches that use the
-//     prefetching loop: those of at least this many tiles
-//     (dz_table_set_prefetch_min_tiles sets it per table). 0: every launch of a
-//     mode in the mask. With the next tile's loads issued half-way, the
-//     prefetching loop is also the faster one for a short pass (OPT-2.7B fp16,
-//     77 K tiles, in the ZO step: 1.544-1.545 against 1.562-1.563 ms).
-// Both masks can be set per mode with -D; the slice loop takes precedence.
-#ifndef DZ_RMW_PREFETCH_MASK
-#define DZ_RMW_PREFETCH_MASK ((1 << (4 * 1 + 3)) | (1 << (4 * 2 + 3)))
-#endif
-#ifndef DZ_RMW_SLICE_MASK
-#define DZ_RMW_SLICE_MASK 0
-#endif
-// The bf16 reverse pass's quotient by one multiply with fp32(1 / alpha) (0:
-// the IEEE division for every element; the values are the same).
-#ifndef DZ_PROJ_RECIP_DIV
-#define DZ_PROJ_RECIP_DIV 1
-#endif
-#ifndef DZ_RMW_PREFETCH_MIN_TILES
-#define DZ_RMW_PREFETCH_MIN_TILES 0
-#endif
-constexpr int kCounters = DZ_RMW_COUNTERS;
-constexpr int kSliceCounters = 16;
-constexpr int kDoneSlot = kCounters > kSliceCounters ? kCounters : kSliceCounters;
+// not overlap in time. Four counters stream as fast as eight at OPT-13B
+// (every mode within 0.3 %), sixteen 0.6-1.2 % slower; a single counter
+// serialises at about 11 ns per atomic.
+constexpr int kCounters = 8;
+constexpr int kDoneSlot = kCounters;
 constexpr int kCounterStride = 32;  // uint32 slots (128 bytes)
 constexpr int kCounterWords = (kDoneSlot + 1) * kCounterStride;
 
-// Projection kernel geometry: persistent 1024-thread workgroups, DZ_PROJ_WG_PER_CU
-// per CU, taking 32768-element chunks (64 KB of theta and 64 KB of theta0 in
-// 16-bit T): each thread 4 (16-bit T) or 8 (fp32) 16-byte vectors of each.
-#ifndef DZ_PROJ_THREADS
-#define DZ_PROJ_THREADS 1024
-#endif
-#ifndef DZ_PROJ_CHUNK
-#define DZ_PROJ_CHUNK 32768
-#endif
-#ifndef DZ_PROJ_WG_PER_CU
-#define DZ_PROJ_WG_PER_CU 1
-#endif
-constexpr int kProjThreads = DZ_PROJ_THREADS;
-constexpr int kProjChunk = DZ_PROJ_CHUNK;
+// Tile loops of the RMW launches. The 16-bit restore + update + next
+// perturbation passes, whose ALU work per tile is the largest, run the
+// prefetching loop (rmw_tiles_prefetch: the next full tile's loads go out
+// half-way through each tile's work). Measured on the MI355X, same box,
+// alternating builds: OPT-13B fp16 7.86-7.90 -> 7.58-7.61 ms, OPT-30B bf16
+// 20.10-20.16 -> 19.83-19.95 ms. The single-Philox passes run the same on
+// either loop (OPT-13B fp16 perturb 7.66-7.69 ms both, OPT-30B bf16 17.76 ms
+// both) and keep the plain loop (rmw_tiles), as does fp32.
+__host__ __device__ constexpr bool rmw_prefetch_mode(int dtype, int mode) {
+  return dtype != DZ_F32 && mode == kModeRestoreUpdatePerturb;
+}
+// A table's default for the launches that use the prefetching loop: those of
+// at least this many tiles (dz_table_set_prefetch_min_tiles sets it per
+// table). 0: every launch of such a mode. With the next tile's loads issued
+// half-way, the prefetching loop is also the faster one for a short pass
+// (OPT-2.7B fp16, 77 K tiles, in the ZO step: 1.544-1.545 against
+// 1.562-1.563 ms).
+constexpr uint32_t kPrefetchMinTilesDefault = 0;
+
+// Projection kernel geometry: persistent 1024-thread workgroups, one per CU,
+// taking 32768-element chunks (64 KB of theta and 64 KB of theta0 in 16-bit
+// T): each thread 4 (16-bit T) or 8 (fp32) 16-byte vectors of each. Two
+// workgroups per CU streamed slower (6.49 against 6.76 TB/s for a bare
+// two-read-one-write kernel), as did smaller workgroups on one counter.
+constexpr int kProjThreads = 1024;
+constexpr int kProjChunk = 32768;
 // Groups whose alphas a projection workgroup keeps in LDS (16 KB of fp32);
 // beyond that each chunk reads its group's alpha from memory.
 constexpr int kProjAlphaLds = 4096;
@@ -168,10 +124,10 @@ struct LaunchEvents {
   hipEvent_t stop = nullptr;
 };
 
-// The first nfull chunks are full, aligned tiles; the rest are partial or
-// misaligned. prefetch: run the prefetching tile loop where the mode allows
-// it (DZ_RMW_PREFETCH_MASK); the caller sets it for long launches.
-hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t nfull, uint32_t grid,
+// The chunk list holds its full, aligned tiles first; the rest are partial
+// or misaligned. prefetch: run the prefetching tile loop where the mode
+// allows it (rmw_prefetch_mode); the caller sets it for long launches.
+hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
                       const void* qtab, const DzScalars& s, const DzScalarPtrs& p, uint32_t* counters,
                       bool prefetch, hipStream_t st, const LaunchEvents& ev = {});
 // Persistent: `grid` workgroups share the chunks through `counters` (zero

@@ -132,14 +132,13 @@ template <int DT, int MODE>
 struct RmwTraits {
   static constexpr bool kWide = (DT == DZ_F32 || rmw_pair_mode(MODE));
   using E = typename std::conditional<kWide, uint32_t, uint16_t>::type;
-  static constexpr int kGroups = rmw_groups(DT, MODE);
-  static constexpr int kChunk = rmw_chunk_elems(DT, MODE);
-  // Waves per SIMD: 4 with one workgroup per CU (128 VGPRs per lane), 8 when
-  // two workgroups share a CU (64 VGPRs).
-  static constexpr int kWavesPerEU = (kWide || DZ_RMW_NARROW_WG_PER_CU == 1) ? 4 : 8;
-  static constexpr bool kSlices = ((DZ_RMW_SLICE_MASK >> (4 * DT + MODE)) & 1) != 0;
-  static constexpr bool kPrefetch = !kSlices && ((DZ_RMW_PREFETCH_MASK >> (4 * DT + MODE)) & 1) != 0;
+  static constexpr int kGroups = rmw_groups(DT);
+  static constexpr int kChunk = rmw_chunk_elems(DT);
+  static constexpr bool kPrefetch = rmw_prefetch_mode(DT, MODE);
 };
+// Waves per SIMD of an RMW launch: one 1024-thread workgroup per CU, 4 waves
+// per SIMD (up to 128 VGPRs per lane).
+constexpr int kRmwWavesPerEU = 4;
 
 // Table entry for z = +Q_T[i] (qbits = bits of Q_T[i]).
 template <int DT, int MODE>
@@ -417,13 +416,13 @@ __device__ __forceinline__ uint32_t apply_one(uint32_t th, uint32_t h, uint32_t 
 // accesses they would also count against the LDS counter, and every wait for
 // an LDS table lookup would then wait for the tile loads in flight as well.
 typedef __attribute__((address_space(1))) dz_u32x4 dz_global_u32x4;
+typedef __attribute__((address_space(1))) char dz_global_char;
 __device__ __forceinline__ dz_u32x4 ld_stream(const void* p) {
   return __builtin_nontemporal_load((const dz_global_u32x4*)(uintptr_t)p);
 }
 __device__ __forceinline__ void st_stream(void* p, dz_u32x4 v) {
   __builtin_nontemporal_store(v, (dz_global_u32x4*)(uintptr_t)p);
 }
-
 // Wave-uniform copy of a 32-bit value in a scalar register.
 // __builtin_amdgcn_readfirstlane returns a signed int: cast back to uint32_t
 // before widening, or values >= 2^31 would sign-extend.
@@ -458,12 +457,21 @@ __device__ __forceinline__ void lds_barrier() {
 // instruction of its own so that the compiler's wait-counter bookkeeping does
 // not track it, and ticket_wait<N> waits for it explicitly once N more
 // vector-memory operations have been issued behind it (the chunk's loads and
-// stores). Tracked by the compiler, the ticket's result, used at the end of
-// the chunk and merged across the full and partial chunk paths, would be
-// waited for with a wait for every operation in flight. Hidden from the
+// stores). Tracked by the compiler, the ticket's result, read where the full
+// and partial chunk paths merge, is waited for with a wait for every
+// operation in flight (the chunk's stores included). Hidden from the
 // compiler, the ticket only ever makes the compiler's own waits wait for one
 // operation more than they count, never less: vector-memory operations leave
 // the wait counter in issue order.
+//
+// The register the atomic writes is not ready until that wait, which the
+// compiler does not know: nothing between the two statements may read, copy
+// or spill it. ticket_wait takes no operands (a wait that took the ticket as
+// an operand, one per chunk path, made the compiler copy the register into
+// the merged value's register ahead of the wait), and the value is used only
+// through ticket_ready, after the waits. tests/test_kernel_asm.py checks the
+// library's generated code for any instruction between the atomic and its
+// wait that touches the register.
 __device__ __forceinline__ uint32_t ticket_take(uint32_t* counter) {
   uint32_t t;
   asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=&v"(t) : "v"(counter), "v"(1u) : "memory");
@@ -475,6 +483,14 @@ template <int N>
 __device__ __forceinline__ void ticket_wait() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// The ticket as a value the compiler may use: an empty volatile statement
+// that redefines it, placed after the waits. Volatile statements keep their
+// order, so no use of the returned value is scheduled above a wait (a use of
+// the atomic's own output could be: the waits have no operands).
+__device__ __forceinline__ uint32_t ticket_ready(uint32_t t) {
+  asm volatile("" : "+v"(t));
+  return t;
 }
 
 // A chunk descriptor read from LDS is the same for every lane: move it to
@@ -513,50 +529,47 @@ __device__ __forceinline__ bool full_tile(const DzChunk& ch) {
   return ch.n == (uint32_t)RmwTraits<DT, MODE>::kChunk && (ch.meta & kDzMetaAligned) != 0u;
 }
 
-// Lane layouts of a full tile. A thread's groups of 8 elements are g0 + u *
-// kStride for u < G (chunk-local group indices), so each load instruction of
-// the kStride threads that share a layout covers contiguous memory:
-//   workgroup layout: kStride = 1024, g0 = threadIdx.x (the workgroup takes
-//                     the whole tile);
-//   slice layout:     kStride = 64, g0 = first + lane (a wave takes the 64 * G
-//                     groups of one slice of the tile, starting at `first`).
-// Byte offset of vector i: group u = i (16-bit) or i / 2 (fp32, two vectors
-// per group).
-template <int DT, int kStride>
-__device__ __forceinline__ size_t tile_vec_offset(uint32_t g0, int i) {
-  if constexpr (DT != DZ_F32) {
-    return (size_t)(g0 + (uint32_t)i * kStride) * 16;
-  } else {
-    return (size_t)(g0 + (uint32_t)(i >> 1) * kStride) * 32 + (size_t)(i & 1) * 16;
+// Lane layout of a full tile: a thread's groups of 8 elements are
+// threadIdx.x + u * 1024 for u < G (tile-local group indices), so each load
+// instruction of the workgroup covers contiguous memory. at(i) is the byte
+// offset of the thread's vector i from the tile's start: group u = i (16-bit)
+// or i / 2 (fp32, two vectors per group). A tile holds at most 64 KB. The
+// offsets are loop-invariant 64-bit values, so each access adds one to the
+// tile's base (one v_lshl_add_u64).
+template <int DT, int MODE>
+struct TileOffsets {
+  __device__ __forceinline__ size_t at(int i) const {
+    const size_t g0 = threadIdx.x;
+    return DT != DZ_F32 ? (g0 + (size_t)i * kRmwThreads) * 16 : (g0 + (size_t)(i >> 1) * kRmwThreads) * 32 + (size_t)(i & 1) * 16;
   }
-}
+};
 
-template <int DT, int MODE, int kStride>
-__device__ __forceinline__ void load_tile_at(uint64_t addr, uint32_t g0, TileRegs<DT, MODE>& r) {
-  const char* base = (const char*)addr;
+template <int DT, int MODE>
+__device__ __forceinline__ void load_tile_at(uint64_t addr, const TileOffsets<DT, MODE>& to, TileRegs<DT, MODE>& r) {
 #pragma unroll
-  for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_stream(base + tile_vec_offset<DT, kStride>(g0, i));
+  for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_stream((const char*)addr + to.at(i));
 }
 
-// Philox block of group g0 + u * kStride: counter zgroup + that group.
-// kUniformHi: the counters' high words agree across the span of groups the
-// layout covers (the low word does not wrap there), so the high word is
-// wave-uniform and round 0's xor and round 1's first product run on the
-// scalar unit, one v_mad_u64_u32 less per block.
-template <bool kUniformHi, int kStride>
-__device__ __forceinline__ DzU4 tile_block(const DzChunk& ch, uint64_t seed, uint32_t g0, int u) {
+// Philox block of group threadIdx.x + u * 1024 of a tile: counter zgroup +
+// that group. kUniformHi: the counters' high words agree across the tile (the
+// low word does not wrap inside it), so the high word is wave-uniform and the
+// counter's other uniform words keep round 0 and a product of rounds 1 and 2
+// on the scalar unit.
+template <bool kUniformHi>
+__device__ __forceinline__ DzU4 tile_block(const DzChunk& ch, uint64_t seed, int u) {
+  const uint32_t g = threadIdx.x + (uint32_t)u * kRmwThreads;
   if constexpr (kUniformHi) {
-    const uint32_t lo = (uint32_t)ch.zgroup + g0 + (uint32_t)u * kStride;
-    return dz_philox_counter(seed, kDzStreamParam, lo, (uint32_t)(ch.zgroup >> 32));
+    return dz_philox_counter(seed, kDzStreamParam, (uint32_t)ch.zgroup + g, (uint32_t)(ch.zgroup >> 32));
   } else {
-    return dz_philox_group(seed, kDzStreamParam, ch.zgroup + g0 + (uint32_t)u * kStride);
+    return dz_philox_group(seed, kDzStreamParam, ch.zgroup + g);
   }
 }
 
 // Group u of a full fp32 tile with its z words w (and next-step words w2):
 // the launch's operation applied and the group stored.
-template <int DT, int MODE, int kStride>
-__device__ __forceinline__ void apply_store_group32(char* base, uint32_t g0, const TileRegs<DT, MODE>& r, int u,
+template <int DT, int MODE>
+__device__ __forceinline__ void apply_store_group32(uint64_t base, const TileOffsets<DT, MODE>& to,
+                                                    const TileRegs<DT, MODE>& r, int u,
                                                     const DzU4& w, const DzU4& w2,
                                                     const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc) {
   const dz_u32x4 a = r.v[2 * u], b = r.v[2 * u + 1];
@@ -569,8 +582,8 @@ __device__ __forceinline__ void apply_store_group32(char* base, uint32_t g0, con
   o1.y = apply_one<DT, MODE>(b.y, w.z >> 16, w2.z >> 16, tab, sc);
   o1.z = apply_one<DT, MODE>(b.z, w.w & 0xffffu, w2.w & 0xffffu, tab, sc);
   o1.w = apply_one<DT, MODE>(b.w, w.w >> 16, w2.w >> 16, tab, sc);
-  st_stream(base + tile_vec_offset<DT, kStride>(g0, 2 * u), o0);
-  st_stream(base + tile_vec_offset<DT, kStride>(g0, 2 * u + 1), o1);
+  st_stream((char*)base + to.at(2 * u), o0);
+  st_stream((char*)base + to.at(2 * u + 1), o1);
 }
 
 // A thread's share of a full tile as one straight-line block: the Philox
@@ -591,77 +604,83 @@ __device__ __forceinline__ void apply_store_group32(char* base, uint32_t g0, con
 // tile's reads meet this tile's first stores in the memory system (rocprofv3
 // counts 18 % fewer reads in flight and 2.7 times the L2 tag stalls per
 // cycle of the perturb pass).
-template <int DT, int MODE, bool kUniformHi, int kStride, bool kLoadNext = false>
-__device__ __forceinline__ void tile_body(const DzChunk& ch, uint32_t g0, const TileRegs<DT, MODE>& r,
+template <int DT, int MODE, bool kUniformHi, bool kLoadNext = false>
+__device__ __forceinline__ void tile_body(const DzChunk& ch, const TileOffsets<DT, MODE>& to,
+                                          const TileRegs<DT, MODE>& r,
                                           const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
                                           uint64_t nptr = 0, TileRegs<DT, MODE>* nxt = nullptr) {
   constexpr int G = RmwTraits<DT, MODE>::kGroups;
   // the next tile's loads go out after group kLoadAfter's stores (-1: first)
   constexpr int kLoadAfter = G > 1 ? G / 2 - 1 : -1;
   if constexpr (kLoadNext && kLoadAfter < 0) {
-    load_tile_at<DT, MODE, kStride>(nptr, g0, *nxt);
+    load_tile_at<DT, MODE>(nptr, to, *nxt);
     __builtin_amdgcn_sched_barrier(0);
   }
   constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
-  char* base = (char*)ch.ptr;
+  const uint64_t base = ch.ptr;
   DzU4 w[G], w2[G];
 #pragma unroll
   for (int u = 0; u < G; ++u) {
-    w[u] = tile_block<kUniformHi, kStride>(ch, sc.seed, g0, u);
-    w2[u] = kTwoSeeds ? tile_block<kUniformHi, kStride>(ch, sc.seed2, g0, u) : w[u];
+    w[u] = tile_block<kUniformHi>(ch, sc.seed, u);
+    w2[u] = kTwoSeeds ? tile_block<kUniformHi>(ch, sc.seed2, u) : w[u];
   }
 #pragma unroll
   for (int u = 0; u < G; ++u) {
     if constexpr (DT == DZ_F32) {
-      apply_store_group32<DT, MODE, kStride>(base, g0, r, u, w[u], w2[u], tab, sc);
+      apply_store_group32<DT, MODE>(base, to, r, u, w[u], w2[u], tab, sc);
     } else {
       dz_u32x4 o;
       o.x = combine_pair16<DT, MODE>(r.v[u].x, w[u].x, w2[u].x, lookup_pair16<DT, MODE>(w[u].x, w2[u].x, tab));
       o.y = combine_pair16<DT, MODE>(r.v[u].y, w[u].y, w2[u].y, lookup_pair16<DT, MODE>(w[u].y, w2[u].y, tab));
       o.z = combine_pair16<DT, MODE>(r.v[u].z, w[u].z, w2[u].z, lookup_pair16<DT, MODE>(w[u].z, w2[u].z, tab));
       o.w = combine_pair16<DT, MODE>(r.v[u].w, w[u].w, w2[u].w, lookup_pair16<DT, MODE>(w[u].w, w2[u].w, tab));
-      st_stream(base + tile_vec_offset<DT, kStride>(g0, u), o);
+      st_stream((char*)base + to.at(u), o);
     }
     if constexpr (kLoadNext && kLoadAfter >= 0) {
       if (u == kLoadAfter) {
         __builtin_amdgcn_sched_barrier(0);
-        load_tile_at<DT, MODE, kStride>(nptr, g0, *nxt);
+        load_tile_at<DT, MODE>(nptr, to, *nxt);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
 }
 
+// Whether the Philox counters of a full tile's groups share their high word
+// (the low word does not wrap inside the tile).
+template <int DT, int MODE>
+__device__ __forceinline__ bool tile_counters_share_high_word(const DzChunk& ch) {
+  constexpr uint32_t kSpan = (uint32_t)(RmwTraits<DT, MODE>::kGroups * kRmwThreads);
+  return (uint32_t)ch.zgroup <= 0xffffffffu - (kSpan - 1u);
+}
+
 // Applies the launch's operation to a thread's share of a full tile, already
-// in registers, and stores it. The layout covers groups first .. first +
-// G * kStride - 1 of the tile.
-template <int DT, int MODE, int kStride>
-__device__ __forceinline__ void compute_store_tile(const DzChunk& ch, uint32_t g0, uint32_t first,
+// in registers, and stores it.
+template <int DT, int MODE>
+__device__ __forceinline__ void compute_store_tile(const DzChunk& ch, const TileOffsets<DT, MODE>& to,
                                                    const TileRegs<DT, MODE>& r,
                                                    const typename RmwTraits<DT, MODE>::E* tab,
                                                    const DzScalars& sc) {
-  constexpr int G = RmwTraits<DT, MODE>::kGroups;
-  if ((uint32_t)ch.zgroup + first <= 0xffffffffu - (uint32_t)(G * kStride - 1) &&
-      (uint32_t)ch.zgroup + first >= (uint32_t)ch.zgroup) {
-    tile_body<DT, MODE, true, kStride>(ch, g0, r, tab, sc);
+  if (tile_counters_share_high_word<DT, MODE>(ch)) {
+    tile_body<DT, MODE, true>(ch, to, r, tab, sc);
   } else {
-    tile_body<DT, MODE, false, kStride>(ch, g0, r, tab, sc);
+    tile_body<DT, MODE, false>(ch, to, r, tab, sc);
   }
 }
 
-// Partial or misaligned tile, bounds-checked: groups first + lane, first +
-// lane + kStride, ... below `end` (and inside the tile). In a 16-byte-aligned
-// tensor a group with all 8 elements inside the tile goes through vector
-// loads and stores like a full tile's; the tensor's last, incomplete group
-// and every group of a misaligned view go element by element.
-template <int DT, int MODE, int kStride>
-__device__ __forceinline__ void rmw_partial(const DzChunk& ch, uint32_t first, uint32_t end, uint32_t lane,
-                                            const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc) {
+// Partial or misaligned tile, bounds-checked: groups threadIdx.x,
+// threadIdx.x + 1024, ... of the tile. In a 16-byte-aligned tensor a group
+// with all 8 elements inside the tile goes through vector loads and stores
+// like a full tile's; the tensor's last, incomplete group and every group of
+// a misaligned view go element by element.
+template <int DT, int MODE>
+__device__ __forceinline__ void rmw_partial(const DzChunk& ch, const typename RmwTraits<DT, MODE>::E* tab,
+                                            const DzScalars& sc) {
   using S = typename DT_<DT>::S;
   constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
   char* base = (char*)ch.ptr;
   const bool aligned = (ch.meta & kDzMetaAligned) != 0u;
-  for (uint32_t g = first + lane; g < end && g * 8u < ch.n; g += kStride) {
+  for (uint32_t g = threadIdx.x; g * 8u < ch.n; g += kRmwThreads) {
     const DzU4 w = dz_philox_group(sc.seed, kDzStreamParam, ch.zgroup + g);
     const DzU4 w2 = kTwoSeeds ? dz_philox_group(sc.seed2, kDzStreamParam, ch.zgroup + g) : w;
     if (aligned && (g + 1u) * 8u <= ch.n) {
@@ -704,80 +723,29 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, uint32_t first, u
 // ---------------------------------------------------------------------------
 // Multi-tensor read-modify-write kernel (perturb / update / restore+update).
 // Persistent workgroups (one per CU) build the launch's delta table in LDS,
-// then take work from the table's counters, handed out dynamically: that
+// then take tiles from the table's counters, handed out dynamically: that
 // keeps the work in flight close together in memory and lets fast
 // workgroups take more, which a static grid-stride split does not. The
-// chunk list holds its nfull full, aligned tiles first. The last workgroup to
-// finish resets the counters for the next launch.
+// workgroup takes whole tiles from counters j of K = min(8, grid / 8),
+// workgroup b using counter (b / 8) mod K, so every counter serves
+// workgroups on every XCD; wave 0 keeps a ring in LDS (while tile k streams,
+// the index of tile k+3 is taken and the descriptor of tile k+2 is loaded,
+// with scalar loads) and a barrier ends each tile. The chunk list holds its
+// nfull full, aligned tiles first. The last workgroup to finish resets the
+// counters for the next launch.
 //
-// Three loops, chosen per mode at compile time (DZ_RMW_SLICE_MASK,
-// DZ_RMW_PREFETCH_MASK) and, for the prefetching one, per launch by size:
-//
-// Wave-level loop (RmwTraits::kSlices; off by default): each wave takes slices of 64 * G
-// groups (a sixteenth of a tile; slice id = ticket * K + j from counter j of
-// the K = 16 slice counters, wave w of every workgroup using counter w mod K,
-// so every counter serves waves on every XCD) and loads, computes and stores
-// them on its own, with no barrier between slices: while one wave waits for
-// memory, the other waves of its SIMD compute. With a barrier per
-// tile, all 16 waves of a workgroup load, wait, compute and store in step,
-// and a tile's load latency and its compute add up instead of overlapping.
-//
-// Workgroup-level loop (rmw_tiles): the workgroup takes whole tiles from
-// counters j of K = min(8, grid / 8), workgroup b using counter (b / 8) mod
-// K; wave 0 keeps a ring in LDS (while tile k streams, the index of tile k+3
-// is taken and the descriptor of tile k+2 is loaded) and a barrier ends each
-// tile.
-//
-// Prefetching workgroup-level loop (rmw_tiles_prefetch, the 16-bit
-// restore+update+next perturb passes; a table can set a minimum launch
-// size, dz_table_set_prefetch_min_tiles): the same tiles and
-// ring, with the next full tile's loads issued half-way through each
-// tile's work; it hands the workgroup's remaining tiles to rmw_tiles at its
-// first tile that is not full.
+// Two tile loops: the plain loop (rmw_tiles) loads each tile when its turn
+// comes; the prefetching loop (rmw_tiles_prefetch, the 16-bit restore +
+// update + next perturb passes; a table can set a minimum launch size,
+// dz_table_set_prefetch_min_tiles) issues the next full tile's loads
+// half-way through each tile's work, and hands the workgroup's remaining
+// tiles to rmw_tiles at its first tile that is not full.
 // ---------------------------------------------------------------------------
-template <int DT, int MODE>
-__device__ __forceinline__ void rmw_slice(const DzChunk& ch, uint32_t c, uint32_t nfull, uint32_t first,
-                                          uint32_t lane, TileRegs<DT, MODE>& r,
-                                          const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc) {
-  constexpr uint32_t G = RmwTraits<DT, MODE>::kGroups;
-  if (c < nfull) {
-    load_tile_at<DT, MODE, 64>(ch.ptr, first + lane, r);
-    compute_store_tile<DT, MODE, 64>(ch, first + lane, first, r, tab, sc);
-  } else {
-    rmw_partial<DT, MODE, 64>(ch, first, first + 64u * G, lane, tab, sc);
-  }
-}
-
-template <int DT, int MODE>
-__device__ __forceinline__ void rmw_slices(const DzChunk* __restrict__ chunks, uint32_t nchunks, uint32_t nfull,
-                                           const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
-                                           uint32_t* __restrict__ counters) {
-  constexpr uint32_t G = RmwTraits<DT, MODE>::kGroups;
-  constexpr uint32_t kSlices = kRmwThreads / 64;  // slices per tile
-  constexpr uint32_t ncnt = (uint32_t)kSliceCounters;
-  static_assert(kSliceCounters <= kRmwThreads / 64, "every slice counter needs a wave of workgroup 0");
-  const uint32_t wave = rfl_u32(threadIdx.x >> 6);
-  const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t j = wave % ncnt;
-  uint32_t* mine = counters + j * kCounterStride;
-  const uint64_t nslices = (uint64_t)nchunks * kSlices;
-  TileRegs<DT, MODE> r;
-  for (;;) {
-    uint32_t t = 0;
-    if (lane == 0) t = atomicAdd(mine, 1u);
-    const uint64_t sid = (uint64_t)rfl_u32(t) * ncnt + j;  // lane 0 is the first active lane
-    if (sid >= nslices) break;
-    const uint32_t c = (uint32_t)(sid / kSlices);
-    const DzChunk ch = uniform_chunk(chunks[c]);
-    rmw_slice<DT, MODE>(ch, c, nfull, (uint32_t)(sid % kSlices) * 64u * G, lane, r, tab, sc);
-  }
-}
-
 template <int DT, int MODE>
 __device__ __forceinline__ void rmw_tiles(uint32_t k0, const DzChunk* __restrict__ chunks, uint32_t nchunks,
                                           const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
-                                          uint32_t* sidx, DzChunk* sdesc, uint32_t* mine, uint32_t ncnt,
-                                          uint32_t j) {
+                                          const TileOffsets<DT, MODE>& to, uint32_t* sidx, DzChunk* sdesc,
+                                          uint32_t* mine, uint32_t ncnt, uint32_t j) {
   const uint64_t nch = nchunks;
   TileRegs<DT, MODE> cur;
   for (uint32_t k = k0;; ++k) {
@@ -804,10 +772,10 @@ __device__ __forceinline__ void rmw_tiles(uint32_t k0, const DzChunk* __restrict
       }
     }
     if (full_tile<DT, MODE>(ch)) {
-      load_tile_at<DT, MODE, kRmwThreads>(ch.ptr, threadIdx.x, cur);
-      compute_store_tile<DT, MODE, kRmwThreads>(ch, threadIdx.x, 0u, cur, tab, sc);
+      load_tile_at<DT, MODE>(ch.ptr, to, cur);
+      compute_store_tile<DT, MODE>(ch, to, cur, tab, sc);
     } else {
-      rmw_partial<DT, MODE, kRmwThreads>(ch, 0u, 0xffffffffu, threadIdx.x, tab, sc);
+      rmw_partial<DT, MODE>(ch, tab, sc);
     }
     if (threadIdx.x == 0) {
       sidx[(k + 3) % 4] = (uint32_t)min((uint64_t)grabbed * ncnt + j, nch);
@@ -824,14 +792,6 @@ __device__ __forceinline__ void rmw_tiles(uint32_t k0, const DzChunk* __restrict
   }
 }
 
-// Whether the Philox counters of a full tile's groups share their high word
-// (the low word does not wrap inside the tile).
-template <int DT, int MODE>
-__device__ __forceinline__ bool tile_counters_share_high_word(const DzChunk& ch) {
-  constexpr uint32_t kSpan = (uint32_t)(RmwTraits<DT, MODE>::kGroups * kRmwThreads);
-  return (uint32_t)ch.zgroup <= 0xffffffffu - (kSpan - 1u);
-}
-
 // A wait for every vector-memory operation in flight that the compiler sees
 // (s_waitcnt with vmcnt 0 and the other counters at their maximum, gfx9
 // encoding), so its own bookkeeping knows that nothing is pending after it.
@@ -846,10 +806,9 @@ __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F7
 template <int DT, int MODE>
 __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk* __restrict__ chunks, uint32_t nchunks,
                                                   const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
-                                                  uint32_t* sidx, DzChunk* sdesc, uint32_t* mine, uint32_t ncnt,
-                                                  uint32_t j, const void* dummy, const TileRegs<DT, MODE>& cur,
-                                                  TileRegs<DT, MODE>& nxt) {
-  constexpr int kVecs = TileRegs<DT, MODE>::kVecs;
+                                                  const TileOffsets<DT, MODE>& to, uint32_t* sidx, DzChunk* sdesc,
+                                                  uint32_t* mine, uint32_t ncnt, uint32_t j, const void* dummy,
+                                                  const TileRegs<DT, MODE>& cur, TileRegs<DT, MODE>& nxt) {
   const DzChunk ch = uniform_chunk(sdesc[k % 3]);
   const uint32_t c1 = rfl_u32(sidx[(k + 1) % 4]);
   const DzChunk ch1 = uniform_chunk(sdesc[(k + 1) % 3]);
@@ -861,7 +820,7 @@ __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk* __r
   uint32_t n_n = 0, n_meta = 0;
   bool have_desc = false;
   if ((rfl_u32(threadIdx.x) >> 6) == 0) {  // wave 0 (uniform branch)
-    if (threadIdx.x == 0) grabbed = ticket_take(mine);
+    if (threadIdx.x == 0) grabbed = atomicAdd(mine, 1u);
     const uint32_t cd = rfl_u32(sidx[(k + 2) % 4]);
     if (cd < nchunks) {
       const DzChunk* src = chunks + cd;
@@ -872,9 +831,11 @@ __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk* __r
       have_desc = true;
     }
   }
-  tile_body<DT, MODE, true, kRmwThreads, true>(ch, threadIdx.x, cur, tab, sc, nptr, &nxt);
+  tile_body<DT, MODE, true, true>(ch, to, cur, tab, sc, nptr, &nxt);
+  // The ticket is first read here, one straight block after the atomic, so
+  // the compiler's wait for it counts the tile's stores and the next tile's
+  // loads issued behind it (vmcnt(2 * kVecs)) instead of draining them.
   if (threadIdx.x == 0) {
-    ticket_wait<2 * kVecs>();  // behind the ticket: tile k + 1's loads and tile k's stores
     sidx[(k + 3) % 4] = (uint32_t)min((uint64_t)grabbed * ncnt + j, (uint64_t)nchunks);
     if (have_desc) {
       DzChunk& d = sdesc[(k + 2) % 3];
@@ -894,16 +855,16 @@ __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk* __r
 // tiles first); the rest of its tiles go through rmw_tiles. Two register
 // sets are used in turn (the loop unrolled by two, so no pending registers
 // are copied); each step is one straight block whose loads go out at a fixed
-// point of it; the ticket is hidden from the compiler (ticket_take); and
-// the barrier orders LDS only. With those, the compiler's waits for a tile's
+// point of it; the ticket is first read in the same straight block as its
+// atomic; and the barrier orders LDS only. With those, the compiler's waits for a tile's
 // data count the operations behind it (the previous tile's stores and the
 // next tile's loads) instead of draining everything in flight.
 template <int DT, int MODE>
 __device__ __forceinline__ uint32_t rmw_tiles_prefetch(const DzChunk* __restrict__ chunks, uint32_t nchunks,
                                                        const typename RmwTraits<DT, MODE>::E* tab,
-                                                       const DzScalars& sc, uint32_t* sidx, DzChunk* sdesc,
-                                                       uint32_t* mine, uint32_t ncnt, uint32_t j,
-                                                       const void* dummy) {
+                                                       const DzScalars& sc, const TileOffsets<DT, MODE>& to,
+                                                       uint32_t* sidx, DzChunk* sdesc, uint32_t* mine, uint32_t ncnt,
+                                                       uint32_t j, const void* dummy) {
   const uint32_t c0 = rfl_u32(sidx[0]);
   const DzChunk ch0 = uniform_chunk(sdesc[0]);
   if (!(c0 < nchunks && full_tile<DT, MODE>(ch0) && tile_counters_share_high_word<DT, MODE>(ch0))) return 0;
@@ -911,14 +872,15 @@ __device__ __forceinline__ uint32_t rmw_tiles_prefetch(const DzChunk* __restrict
   // tile's size)
   static_assert(RmwTraits<DT, MODE>::kChunk <= kDzTabEntries, "the quantile table is a tile's stand-in");
   TileRegs<DT, MODE> a, b;
-  load_tile_at<DT, MODE, kRmwThreads>(ch0.ptr, threadIdx.x, a);
+  load_tile_at<DT, MODE>(ch0.ptr, to, a);
   uint32_t k = 0;
   for (;;) {
-    if (!rmw_prefetch_step<DT, MODE>(k, chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j, dummy, a, b)) {
+    if (!rmw_prefetch_step<DT, MODE>(k, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j, dummy, a, b)) {
       k += 1;
       break;
     }
-    if (!rmw_prefetch_step<DT, MODE>(k + 1, chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j, dummy, b, a)) {
+    if (!rmw_prefetch_step<DT, MODE>(k + 1, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j, dummy, b,
+                                     a)) {
       k += 2;
       break;
     }
@@ -931,59 +893,52 @@ __device__ __forceinline__ uint32_t rmw_tiles_prefetch(const DzChunk* __restrict
 // kPF: run the prefetching tile loop over the workgroup's leading full tiles
 // (only where RmwTraits::kPrefetch allows it; the launcher picks it by size).
 template <int DT, int MODE, bool kPF>
-__global__ void __launch_bounds__(kRmwThreads, (RmwTraits<DT, MODE>::kWavesPerEU)) rmw_kernel(const DzChunk* __restrict__ chunks,
-                                                          uint32_t nchunks, uint32_t nfull,
-                                                          const void* __restrict__ qtab,
-                                                          DzScalars sc_in, DzScalarPtrs sp,
-                                                          uint32_t* __restrict__ counters) {
+__global__ void __launch_bounds__(kRmwThreads, kRmwWavesPerEU) rmw_kernel(const DzChunk* __restrict__ chunks,
+                                                                          uint32_t nchunks,
+                                                                          const void* __restrict__ qtab,
+                                                                          DzScalars sc_in, DzScalarPtrs sp,
+                                                                          uint32_t* __restrict__ counters) {
   using Tr = RmwTraits<DT, MODE>;
   using E = typename Tr::E;
   __shared__ __attribute__((aligned(16))) E tab[kDzTabEntries];
+  // Tile bookkeeping rings: indices of tiles k .. k+3, descriptors of k .. k+2.
+  __shared__ uint32_t sidx[4];
+  __shared__ DzChunk sdesc[3];
   const DzScalars sc = resolve_scalars<DT>(sc_in, sp);
-  if constexpr (Tr::kSlices) {
-    TableSlices<DT> qs;
-    load_table<DT>(qs, qtab);
-    store_table<DT, MODE>(tab, qs, sc);
-    __syncthreads();
-    rmw_slices<DT, MODE>(chunks, nchunks, nfull, tab, sc, counters);
-    __syncthreads();  // every wave of the workgroup has taken its last ticket
-  } else {
-    // Tile bookkeeping rings: indices of tiles k .. k+3, descriptors of k .. k+2.
-    __shared__ uint32_t sidx[4];
-    __shared__ DzChunk sdesc[3];
-    // Counters in use: every one of them must be served by at least one
-    // workgroup, or its tiles would never be taken (a small grid uses fewer).
-    const uint32_t ncnt = rfl_u32(max(1u, min((uint32_t)kCounters, gridDim.x >> 3)));
-    const uint32_t j = rfl_u32((blockIdx.x >> 3) % ncnt);
-    uint32_t* mine = counters + j * kCounterStride;
-    const uint64_t nch = nchunks;
-    // Start-up: lane 0 takes the first three tickets with one atomic, the
-    // table's loads are issued behind it, then the first two descriptors are
-    // loaded (clamped to a valid index; only tickets below nchunks are used)
-    // and the table is written.
-    uint32_t t0 = 0;
-    if (threadIdx.x == 0) t0 = atomicAdd(mine, 3u);
-    TableSlices<DT> qs;
-    load_table<DT>(qs, qtab);
-    if (threadIdx.x == 0) {
-      uint64_t c[3];
-      for (int i = 0; i < 3; ++i) {
-        c[i] = (uint64_t)(t0 + i) * ncnt + j;
-        sidx[i] = (uint32_t)min(c[i], nch);
-      }
-      if (nch > 0) {
-        const DzChunk d0 = chunks[min(c[0], nch - 1)];
-        const DzChunk d1 = chunks[min(c[1], nch - 1)];
-        sdesc[0] = d0;
-        sdesc[1] = d1;
-      }
+  // Counters in use: every one of them must be served by at least one
+  // workgroup, or its tiles would never be taken (a small grid uses fewer).
+  const uint32_t ncnt = rfl_u32(max(1u, min((uint32_t)kCounters, gridDim.x >> 3)));
+  const uint32_t j = rfl_u32((blockIdx.x >> 3) % ncnt);
+  uint32_t* mine = counters + j * kCounterStride;
+  const uint64_t nch = nchunks;
+  // Start-up: lane 0 takes the first three tickets with one atomic, the
+  // table's loads are issued behind it, then the first two descriptors are
+  // loaded (clamped to a valid index; only tickets below nchunks are used)
+  // and the table is written.
+  uint32_t t0 = 0;
+  if (threadIdx.x == 0) t0 = atomicAdd(mine, 3u);
+  TableSlices<DT> qs;
+  load_table<DT>(qs, qtab);
+  if (threadIdx.x == 0) {
+    uint64_t c[3];
+    for (int i = 0; i < 3; ++i) {
+      c[i] = (uint64_t)(t0 + i) * ncnt + j;
+      sidx[i] = (uint32_t)min(c[i], nch);
     }
-    store_table<DT, MODE>(tab, qs, sc);
-    __syncthreads();
-    uint32_t k0 = 0;
-    if constexpr (Tr::kPrefetch && kPF) k0 = rmw_tiles_prefetch<DT, MODE>(chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j, qtab);
-    rmw_tiles<DT, MODE>(k0, chunks, nchunks, tab, sc, sidx, sdesc, mine, ncnt, j);
+    if (nch > 0) {
+      const DzChunk d0 = chunks[min(c[0], nch - 1)];
+      const DzChunk d1 = chunks[min(c[1], nch - 1)];
+      sdesc[0] = d0;
+      sdesc[1] = d1;
+    }
   }
+  store_table<DT, MODE>(tab, qs, sc);
+  const TileOffsets<DT, MODE> to{};
+  __syncthreads();
+  uint32_t k0 = 0;
+  if constexpr (Tr::kPrefetch && kPF)
+    k0 = rmw_tiles_prefetch<DT, MODE>(chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j, qtab);
+  rmw_tiles<DT, MODE>(k0, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j);
   if (threadIdx.x == 0) {
     const uint32_t done = atomicAdd(counters + kDoneSlot * kCounterStride, 1u);
     if (done == gridDim.x - 1) {
@@ -1157,7 +1112,7 @@ __device__ __forceinline__ void proj_chunk(const DzChunk& ch, float alpha, doubl
     constexpr int kVecsPerThread = ProjChunkOps<DT, MODE>::kVecs;
     // alpha in both 16-bit lanes (the ZO modes' alpha is a value of T)
     const uint32_t alpha2 = (kES == 2 && MODE != kProjApplyF32) ? DT_<DT>::from_f(alpha) * 0x10001u : 0u;
-    const RecipDiv rd = (DZ_PROJ_RECIP_DIV && DT == DZ_BF16 && (MODE == kProjReverse || MODE == kProjReverseSumsq))
+    const RecipDiv rd = (DT == DZ_BF16 && (MODE == kProjReverse || MODE == kProjReverseSumsq))
                             ? recip_div(alpha)
                             : RecipDiv{0.0f, false};
     dz_u32x4 vt[kVecsPerThread], va[kVecsPerThread];
@@ -1185,10 +1140,7 @@ __device__ __forceinline__ void proj_chunk(const DzChunk& ch, float alpha, doubl
           o[i] = r;
         }
       }
-      if constexpr (MODE != kProjSumsq) {
-        const size_t off = (size_t)(threadIdx.x + u * kProjThreads) * 16;
-        st_stream(tp + off, o);
-      }
+      if constexpr (MODE != kProjSumsq) st_stream(tp + (size_t)(threadIdx.x + u * kProjThreads) * 16, o);
     }
   } else {
     for (uint32_t e = threadIdx.x; e < ch.n; e += kProjThreads) {
@@ -1292,7 +1244,8 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
       if (threadIdx.x == 0) ticket_wait<0>();
     }
     if (threadIdx.x == 0) {
-      sidx[(k + 3) % 4] = (uint32_t)min((uint64_t)grabbed * ncnt + j, nch);
+      const uint32_t t = ticket_ready(grabbed);
+      sidx[(k + 3) % 4] = (uint32_t)min((uint64_t)t * ncnt + j, nch);
       if (have_desc) {
         DzChunk& d = sdesc[(k + 2) % 3];
         d.ptr = n_ptr;
@@ -1442,30 +1395,30 @@ __global__ void __launch_bounds__(256) philox_kernel(uint64_t seed, uint32_t str
   } while (0)
 
 template <int DT>
-static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t nfull, uint32_t grid,
+static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
                                 const void* tab, const DzScalars& s, const DzScalarPtrs& p,
                                 uint32_t* counters, bool prefetch, hipStream_t st, const LaunchEvents& ev) {
   switch (mode) {
     case kModePerturb:
       DZ_LAUNCH((rmw_kernel<DT, kModePerturb, false>), dim3(grid), dim3(kRmwThreads), st, ev,
-                         chunks, nchunks, nfull, tab, s, p, counters);
+                         chunks, nchunks, tab, s, p, counters);
       break;
     case kModeUpdate:
       DZ_LAUNCH((rmw_kernel<DT, kModeUpdate, false>), dim3(grid), dim3(kRmwThreads), st, ev,
-                         chunks, nchunks, nfull, tab, s, p, counters);
+                         chunks, nchunks, tab, s, p, counters);
       break;
     case kModeRestoreUpdate:
       DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdate, false>), dim3(grid), dim3(kRmwThreads),
-                         st, ev, chunks, nchunks, nfull, tab, s, p, counters);
+                         st, ev, chunks, nchunks, tab, s, p, counters);
       break;
     case kModeRestoreUpdatePerturb:
-      // the caller asks for the prefetching loop on long launches (DZ_RMW_PREFETCH_MIN_TILES)
+      // the caller asks for the prefetching loop on long launches (the table's prefetch_min_tiles)
       if (RmwTraits<DT, kModeRestoreUpdatePerturb>::kPrefetch && prefetch) {
         DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdatePerturb, true>), dim3(grid), dim3(kRmwThreads),
-                           st, ev, chunks, nchunks, nfull, tab, s, p, counters);
+                           st, ev, chunks, nchunks, tab, s, p, counters);
       } else {
         DZ_LAUNCH((rmw_kernel<DT, kModeRestoreUpdatePerturb, false>), dim3(grid), dim3(kRmwThreads),
-                           st, ev, chunks, nchunks, nfull, tab, s, p, counters);
+                           st, ev, chunks, nchunks, tab, s, p, counters);
       }
       break;
     default:
@@ -1474,16 +1427,16 @@ static hipError_t launch_rmw_dt(int mode, const DzChunk* chunks, uint32_t nchunk
   return hipGetLastError();
 }
 
-hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t nfull, uint32_t grid,
+hipError_t launch_rmw(int dtype, int mode, const DzChunk* chunks, uint32_t nchunks, uint32_t grid,
                       const void* tab, const DzScalars& s, const DzScalarPtrs& p, uint32_t* counters,
                       bool prefetch, hipStream_t st, const LaunchEvents& ev) {
   switch (dtype) {
     case DZ_F32:
-      return launch_rmw_dt<DZ_F32>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, prefetch, st, ev);
+      return launch_rmw_dt<DZ_F32>(mode, chunks, nchunks, grid, tab, s, p, counters, prefetch, st, ev);
     case DZ_F16:
-      return launch_rmw_dt<DZ_F16>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, prefetch, st, ev);
+      return launch_rmw_dt<DZ_F16>(mode, chunks, nchunks, grid, tab, s, p, counters, prefetch, st, ev);
     case DZ_BF16:
-      return launch_rmw_dt<DZ_BF16>(mode, chunks, nchunks, nfull, grid, tab, s, p, counters, prefetch, st, ev);
+      return launch_rmw_dt<DZ_BF16>(mode, chunks, nchunks, grid, tab, s, p, counters, prefetch, st, ev);
     default: return hipErrorInvalidValue;
   }
 }

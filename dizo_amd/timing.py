@@ -55,17 +55,23 @@ class KernelTimer:
         self.spans = {}
 
     def summary(self) -> Dict[str, Dict[str, float]]:
-        """Per span name: launches, total / mean device ms, bytes per launch, GB/s."""
+        """Per span name: launches, total / mean / median / min / max device ms,
+        bytes per launch, GB/s (from the total)."""
         torch.cuda.synchronize()
         out = {}
         for name, recs in self.spans.items():
             ms = [a.elapsed_time(b) for a, b, _ in recs]
             nbytes = sum(n for _, _, n in recs)
             tot = sum(ms)
+            srt = sorted(ms)
+            mid = len(srt) // 2
             out[name] = {
                 "launches": len(recs),
                 "total_ms": tot,
                 "mean_ms": tot / len(recs),
+                "median_ms": srt[mid] if len(srt) % 2 else 0.5 * (srt[mid - 1] + srt[mid]),
+                "min_ms": srt[0],
+                "max_ms": srt[-1],
                 "bytes_per_launch": nbytes / len(recs),
                 "GBps": (nbytes / (tot * 1e-3) / 1e9) if tot > 0 else 0.0,
             }

@@ -56,7 +56,8 @@ const char* dz_last_error(void);
  * Replaces the normal transform inside torch.normal, trainer.py:1441,1607. */
 int32_t dz_normal_table(int32_t dtype, void* out, int64_t n_entries);
 
-/* Block of the z generator, Philox4x32-7, for key = seed, counter = (q, stream, 0), on the host. */
+/* Block of the z generator, Philox4x32-7, for key = seed and the counter words
+ * (stream, q mod 2^32, 0, q >> 32), on the host. */
 int32_t dz_philox_host(uint64_t seed, uint32_t stream_id, uint64_t q, uint32_t out[4]);
 
 /* ---- parameter tables --------------------------------------------------- */

@@ -10,7 +10,7 @@ R = 10; z uses R = ROUNDS = 7, the fewest rounds the paper found
 Crush-resistant for Philox4x32 (the library's dz_common.h defines the same).
 
 The z that replaces torch.normal (trainer.py:1441, 1607) is defined as
-  q = e >> 3, j = e & 7, w = Philox4x32-7(counter = (q lo, q hi, stream, 0), key = seed)
+  q = e >> 3, j = e & 7, w = Philox4x32-7(counter = (stream, q lo, 0, q hi), key = seed)
   h = 16-bit field j of w (word j >> 1, half j & 1)
   z = (-1)^(h >> 15) * Q_T[h & 0x7fff],  Q_T[i] = RNE_T(Phi^-1(1/2 + (i + 1/2) / 65536)).
 """
@@ -67,9 +67,10 @@ def philox_scalar(ctr, key, rounds: int = 10):
 
 def philox_groups(seed: int, stream: int, q, rounds: int = ROUNDS) -> np.ndarray:
     """Blocks for counters q (uint64 array) under key = seed: (n, 4) uint32
-    (the z generator's Philox4x32-7 unless `rounds` says otherwise)."""
+    (the z generator's Philox4x32-7 unless `rounds` says otherwise). Counter
+    words: (stream, q lo, 0, q hi)."""
     q = np.asarray(q, dtype=np.uint64)
-    return philox4x32(q & np.uint64(MASK32), q >> np.uint64(32), np.uint64(stream), np.uint64(0),
+    return philox4x32(np.uint64(stream), q & np.uint64(MASK32), np.uint64(0), q >> np.uint64(32),
                       seed & MASK32, (seed >> 32) & MASK32, rounds)
 
 

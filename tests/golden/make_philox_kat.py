@@ -7,9 +7,11 @@ Two independent sources:
     BSD source shipped with the installed torch), compiled with g++ and run
     for a set of (seed, subsequence, offset) triples, with its default 10
     rounds and with 7 (the engine takes the round count as an argument; 7 is
-    the z generator's). That engine keys Philox with the seed and uses
-    counter = (offset, subsequence), so its first output block equals our
-    block for key = seed, counter = (q = offset, stream = subsequence).
+    the z generator's). That engine keys Philox with the seed and uses the
+    counter words (offset lo, offset hi, subsequence lo, subsequence hi), so
+    its first output block equals the z generator's block for key = seed,
+    counter = (stream, q lo, 0, q hi) when offset = stream + 2^32 q lo and
+    subsequence = 2^32 q hi.
 
 Run: python tests/golden/make_philox_kat.py
 """
@@ -32,7 +34,7 @@ RANDOM123_KAT = [
      [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]],
 ]
 
-CASES = [  # (seed, subsequence = stream, offset = q)
+CASES = [  # (seed, stream, q)
     (0, 0, 0), (1, 0, 0), (26, 0, 1), (123456789, 0, 7), (999999999, 1, 12345),
     (2**32 + 3, 2, 2**32 + 11), (2**64 - 1, 0, 2**64 - 1), (42, 1, 2**40), (7, 0, 3_000_000_000),
 ]
@@ -55,6 +57,12 @@ int main(int argc, char** argv) {
 """
 
 
+def engine_args(seed: int, stream: int, q: int):
+    """(seed, subsequence, offset) of at::Philox4_32 whose counter is the z
+    generator's (stream, q lo, 0, q hi)."""
+    return seed, (q >> 32) << 32, stream + ((q & 0xFFFFFFFF) << 32)
+
+
 def torch_engine_blocks(cases, rounds: int = 10):
     inc = os.path.join(os.path.dirname(torch.__file__), "include")
     with tempfile.TemporaryDirectory() as td:
@@ -63,7 +71,7 @@ def torch_engine_blocks(cases, rounds: int = 10):
         with open(src, "w") as f:
             f.write(PROG)
         subprocess.run(["g++", "-O1", "-std=c++17", f"-I{inc}", src, "-o", exe], check=True)
-        args = [str(x) for c in cases for x in c]
+        args = [str(x) for c in cases for x in engine_args(*c)]
         out = subprocess.run([exe, str(rounds), *args], check=True, capture_output=True, text=True).stdout
     return [[int(x) for x in line.split()] for line in out.strip().splitlines()]
 
@@ -73,10 +81,10 @@ def main():
     blocks7 = torch_engine_blocks(CASES, rounds=7)
     data = {
         "random123": RANDOM123_KAT,
-        "torch_engine": [{"seed": s, "stream": sub, "q": off, "block": b}
-                         for (s, sub, off), b in zip(CASES, blocks)],
-        "torch_engine_r7": [{"seed": s, "stream": sub, "q": off, "block": b}
-                            for (s, sub, off), b in zip(CASES, blocks7)],
+        "torch_engine": [{"seed": s, "stream": st, "q": q, "block": b}
+                         for (s, st, q), b in zip(CASES, blocks)],
+        "torch_engine_r7": [{"seed": s, "stream": st, "q": q, "block": b}
+                            for (s, st, q), b in zip(CASES, blocks7)],
         "source": "tests/golden/make_philox_kat.py",
     }
     with open(os.path.join(HERE, "philox_kat.json"), "w") as f:
