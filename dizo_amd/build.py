@@ -12,7 +12,7 @@ import sys
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libdizo_amd.so")
-SOURCES = ["dz_kernels.hip", "dz_attention.hip", "dz_api.hip"]
+SOURCES = ["dz_kernels.hip", "dz_api.hip"]
 HEADERS = ["dz_common.h", "dz_kernels.h"]
 
 # -ffp-contract=off: products must not be contracted into FMAs (bit parity with

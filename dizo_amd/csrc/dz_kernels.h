@@ -166,22 +166,4 @@ hipError_t launch_normals(int dtype, const void* tab, uint64_t seed, uint32_t st
 hipError_t launch_philox(uint64_t seed, uint32_t stream, uint64_t q0, uint64_t n, uint32_t* out,
                          hipStream_t st);
 
-// Causal attention of an unpadded batch (dz_attention.hip). Element offsets:
-// token t of sequence b, head h of q starts at q + b * q_seq + t * q_tok + h * head_dim
-// (the same for k and v); out is (sequences, L, H, head_dim) contiguous.
-struct AttnArgs {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  uint16_t* out;
-  int64_t q_tok, k_tok, v_tok;
-  int64_t q_seq, k_seq, v_seq;
-  int32_t L;
-  int32_t H;
-  float scale;  // q is used as R_T(q * scale)
-};
-size_t attn_lds_bytes(int head_dim, int L);
-// One workgroup per (sequence, head): nblocks = sequences * H.
-hipError_t launch_attn_causal(int dtype, int head_dim, const AttnArgs& a, uint32_t nblocks, hipStream_t st);
-
 }  // namespace dz

@@ -3,10 +3,8 @@
 The ZO step runs two forwards per step (and 20 per DiZO event) without
 autograd, and at OPT-13B those forwards are ~90 % of the step. Two changes to
 how the layer calls its GEMMs make them cheaper and leave every value as HF's
-layer computes it on this stack; the fused attention module also hands an
-unpadded batch's causal attention to the library's kernel when asked
-(`use_library_attention`, dizo_amd.attention; not bit-identical to SDPA), and
-gives SDPA a padded batch's mask in additive form, made once per forward
+layer computes it on this stack; the fused attention module also gives SDPA a
+padded batch's mask in additive form, made once per forward
 (`_additive_mask`; the same bits).
 
 1. fc1 + ReLU (`OPTDecoderLayer.forward`: `fc2(activation_fn(fc1(h)))`, ReLU
@@ -159,12 +157,6 @@ class FusedQKVOPTAttention(_opt.OPTAttention):
         w, b = fused
         bsz, tgt_len, _ = hidden_states.size()
         k, v, q = F.linear(hidden_states, w, b).split(self.embed_dim, dim=-1)
-        if getattr(self, "dz_attention", False) and self._library_attention_applies(attention_mask, q, tgt_len,
-                                                                                     kwargs):
-            from .attention import attention_causal
-
-            out = attention_causal(q, k, v, self.num_heads, self.head_dim, self.scaling)
-            return self.out_proj(out.view(bsz, tgt_len, -1)), None
         if (attention_mask is not None and attention_mask.dtype == torch.bool
                 and self.config._attn_implementation in _SDPA_IMPLS):
             attention_mask = _additive_mask(attention_mask, q.dtype)
@@ -179,16 +171,6 @@ class FusedQKVOPTAttention(_opt.OPTAttention):
             dropout=0.0 if not self.training else self.dropout, scaling=1.0, **kwargs)
         attn_output = attn_output.reshape(bsz, tgt_len, -1).contiguous()
         return self.out_proj(attn_output), attn_weights
-
-    def _library_attention_applies(self, attention_mask, q, tgt_len: int, kwargs) -> bool:
-        """The case dz_attention_causal stands in for: an SDPA-family
-        implementation given no mask (its is_causal path, an unpadded batch),
-        no dropout, no attention weights asked for, a shape the kernel takes."""
-        from .attention import supported
-
-        return (attention_mask is None and not self.training and tgt_len > 1 and getattr(self, "is_causal", True)
-                and self.config._attn_implementation in _SDPA_IMPLS and not kwargs.get("output_attentions", False)
-                and supported(q, tgt_len, self.head_dim))
 
 
 def fuse_qkv(model: nn.Module) -> int:
@@ -221,22 +203,6 @@ def fuse_qkv(model: nn.Module) -> int:
     return n
 
 
-def use_library_attention(model: nn.Module, on: bool = True) -> int:
-    """Routes the fused attention modules' unmasked causal case through
-    libdizo_amd's attention kernel (dizo_amd.attention) instead of SDPA, or
-    back. Returns the number of modules set; modules not in the fused k/v/q
-    form are left as they are."""
-    n = 0
-    for mod in model.modules():
-        if isinstance(mod, FusedQKVOPTAttention):
-            mod.dz_attention = bool(on)
-            n += 1
-    return n
-
-
-def fuse_forward(model: nn.Module, mlp: bool = True, qkv: bool = True, attention: bool = False) -> dict:
-    """The fusions asked for; returns how many layers each changed.
-    `attention` needs the fused k/v/q form (it reads q, k, v from that buffer)."""
-    out = {"mlp": fuse_relu_mlp(model) if mlp else 0, "qkv": fuse_qkv(model) if qkv else 0}
-    out["attention"] = use_library_attention(model) if attention else 0
-    return out
+def fuse_forward(model: nn.Module, mlp: bool = True, qkv: bool = True) -> dict:
+    """The fusions asked for; returns how many layers each changed."""
+    return {"mlp": fuse_relu_mlp(model) if mlp else 0, "qkv": fuse_qkv(model) if qkv else 0}

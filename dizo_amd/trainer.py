@@ -98,10 +98,6 @@ class ZOArguments:
     # the same values where hipBLASLt runs one kernel family for both shapes
     zo_fused_mlp: bool = False
     zo_fused_qkv: bool = False
-    # build-specific: with the fused k/v/q form (implied), run an unpadded
-    # batch's causal attention through the library's kernel instead of SDPA
-    # (dizo_amd.attention; not bit-identical to SDPA's flash kernel)
-    zo_fused_attention: bool = False
     # build-specific: keep a journal of every pass that changes the trainable
     # tensors (seed, g, lr per step; DiZO projections), for exact replay and
     # checkpoints (dizo_amd.checkpoint)
@@ -351,12 +347,11 @@ class ZOTrainerMixin:
             base_model = _anchor_copy(model, self.exclude_list)
         # the fused q/k/v layout moves those weights into new buffers: after the
         # anchor copy, before any table records parameter addresses
-        fused_attn = bool(getattr(args, "zo_fused_attention", False))
-        if getattr(args, "zo_fused_mlp", False) or getattr(args, "zo_fused_qkv", False) or fused_attn:
+        if getattr(args, "zo_fused_mlp", False) or getattr(args, "zo_fused_qkv", False):
             from .fused_layers import fuse_forward
 
             fuse_forward(model, mlp=bool(getattr(args, "zo_fused_mlp", False)),
-                         qkv=bool(getattr(args, "zo_fused_qkv", False)) or fused_attn, attention=fused_attn)
+                         qkv=bool(getattr(args, "zo_fused_qkv", False)))
         if enhanced:
             self.base_model = base_model
             self.dizo_trainer = dizo_trainer(base_model, train_dataloader, "l2norm", 0.1, 10, self.exclude_list)

@@ -42,7 +42,7 @@ def test_fuse_changes_layout_not_names(base):
     vals0 = {k: v.clone() for k, v in b.state_dict().items()}
     got = fuse_forward(b)
     L = SHAPES["opt-tiny"].layers
-    assert got == {"mlp": L, "qkv": L, "attention": 0}
+    assert got == {"mlp": L, "qkv": L}
     assert [n for n, _ in b.named_parameters()] == names0
     assert list(b.state_dict().keys()) == keys0
     for k, v in b.state_dict().items():
@@ -135,7 +135,7 @@ def test_models_of_other_forms_are_left_alone():
                       num_attention_heads=2, num_key_value_heads=1)
     m = LlamaForCausalLM(cfg)
     ptrs = [p.data_ptr() for p in m.parameters()]
-    assert fuse_forward(m, attention=True) == {"mlp": 0, "qkv": 0, "attention": 0}
+    assert fuse_forward(m) == {"mlp": 0, "qkv": 0}
     assert [p.data_ptr() for p in m.parameters()] == ptrs
     gelu = torch.nn.Module()
     gelu.fc1 = torch.nn.Linear(4, 4)
@@ -165,22 +165,6 @@ def test_trainer_applies_the_fusions(base):
     assert type(plain.model.decoder.layers[0].self_attn) is not FusedQKVOPTAttention
 
 
-def test_library_attention_flag_falls_back_off_gpu(base):
-    """use_library_attention marks the fused modules only; on the CPU (or for
-    any case the kernel does not take) the forward is SDPA's, unchanged."""
-    from dizo_amd.fused_layers import use_library_attention
-
-    a = copy.deepcopy(base)
-    b = copy.deepcopy(base)
-    assert use_library_attention(b) == 0  # not fused yet: nothing marked
-    assert fuse_forward(b, attention=True)["attention"] == SHAPES["opt-tiny"].layers
-    assert all(layer.self_attn.dz_attention for layer in b.model.decoder.layers)
-    batch = make_batches(1, 2, 512, seed=6, device="cpu", fixed_len=32)[0]
-    assert torch.equal(_bits(_logits(a, batch)), _bits(_logits(b, batch)))
-    assert use_library_attention(b, on=False) == SHAPES["opt-tiny"].layers
-    assert not any(layer.self_attn.dz_attention for layer in b.model.decoder.layers)
-
-
 @pytest.mark.parametrize("enable_bias,ln_before", [(False, True), (True, False)])
 def test_fusions_on_other_opt_configs(enable_bias, ln_before):
     """OPT without biases (the k/v/q buffer without a bias buffer; fc1 left as
@@ -194,7 +178,7 @@ def test_fusions_on_other_opt_configs(enable_bias, ln_before):
     torch.manual_seed(2)
     a = OPTForCausalLM(cfg).eval()
     b = copy.deepcopy(a)
-    got = fuse_forward(b, attention=True)
+    got = fuse_forward(b)
     assert got["qkv"] == 2 and got["mlp"] == (2 if enable_bias else 0)
     w, bias = qkv_views(b.model.decoder.layers[0].self_attn)
     assert (bias is None) == (not enable_bias)

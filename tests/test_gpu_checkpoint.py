@@ -34,7 +34,7 @@ def _trainer(dt, enhanced, graph=False, journal=True, seed=71, fused=False):
     model = build_opt("opt-tiny", dt, "cuda", seed=seed)
     init = copy.deepcopy(model)
     args = ZOArguments(learning_rate=1e-3, zo_eps=1e-3, max_steps=120, enhanced=enhanced, zo_graph=graph,
-                       zo_journal=journal, zo_fused_mlp=fused, zo_fused_qkv=fused, zo_fused_attention=fused)
+                       zo_journal=journal, zo_fused_mlp=fused, zo_fused_qkv=fused)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(_batches()))
     return tr, model, init
