@@ -59,11 +59,10 @@ SIGNATURES = {
     "dz_export_z": (_i32, [_p, _u64, _i32, _p, _p]),
     "dz_philox": (_i32, [_u64, _u32, _u64, _i64, _p, _p]),
     "dz_group_sumsq": (_i32, [_p, _p, _p, _p, _p]),
+    "dz_init": (_i32, [_i32]),
     "dz_group_sumsq_static": (_i32, [_p, _p, _p, _i32, _i32, _p, _p, _p, _p]),
     "dz_project": (_i32, [_p, _p, _i32, _p, _p, _p, _p]),
     "dz_group_dot": (_i32, [_p, _p, _p, _p, _p]),
-    "dz_attention_causal": (_i32, [_i32, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32,
-                                   _i32, _f32, _p]),
 }
 
 _lock = threading.Lock()

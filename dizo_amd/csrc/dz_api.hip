@@ -428,6 +428,29 @@ int32_t dz_version(void) { return 30000; }
 
 const char* dz_last_error(void) { return g_last_error.c_str(); }
 
+int32_t dz_init(int32_t device) {
+  int dev;
+  int32_t rc = current_device(&dev);
+  if (rc) return rc;
+  if (device != dev) {
+    return fail(DZ_ERR_DEVICE, "dz_init(" + std::to_string(device) + ") with device " + std::to_string(dev) +
+                                   " current");
+  }
+  StaticScratch* sc = nullptr;
+  rc = static_scratch(dev, &sc);
+  if (rc) return rc;
+  // The runtime sets up the library's first kernel launch on a device with an
+  // allocation of its own (2 MiB measured): one launch of the plan kernel
+  // with an empty batch, which returns at once, takes it here.
+  dz::StaticPlanBatch empty{};
+  hipError_t e = dz::launch_static_plan(empty, (DzChunk*)(sc->ptr + kStaticOffChunks),
+                                        (uint32_t*)(sc->ptr + kStaticOffGroupBegin),
+                                        (uint32_t*)(sc->ptr + kStaticOffCounters), nullptr);
+  if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+  if (e != hipSuccess) return hip_fail(e, "dz_init warm-up launch");
+  return DZ_OK;
+}
+
 int32_t dz_normal_table(int32_t dtype, void* out, int64_t n_entries) {
   if (!valid_dtype(dtype)) return fail(DZ_ERR_INVALID, "unknown dtype");
   if (!out) return fail(DZ_ERR_INVALID, "out is NULL");
@@ -808,60 +831,5 @@ int32_t dz_group_dot(dz_table* t, const uint64_t* other_ptrs, double* d_dot, flo
   return DZ_OK;
 }
 
-int32_t dz_attention_causal(int32_t dtype, const void* q, const void* k, const void* v, void* out, int64_t q_tok,
-                            int64_t k_tok, int64_t v_tok, int64_t q_seq, int64_t k_seq, int64_t v_seq,
-                            int32_t n_seq, int32_t L, int32_t H, int32_t head_dim, float scale, void* stream) {
-  if (dtype != DZ_DTYPE_F16 && dtype != DZ_DTYPE_BF16) return fail(DZ_ERR_INVALID, "attention: dtype must be fp16 or bf16");
-  if (head_dim != 64 && head_dim != 128) return fail(DZ_ERR_INVALID, "attention: head_dim must be 64 or 128");
-  if (L < 32 || L > 256 || L % 32 != 0) return fail(DZ_ERR_INVALID, "attention: L must be a multiple of 32 in [32, 256]");
-  if (n_seq < 1 || H < 1 || (int64_t)n_seq * H > 0x7fffffffLL) {
-    return fail(DZ_ERR_INVALID, "attention: n_seq and H must be positive (n_seq * H < 2^31)");
-  }
-  const void* ins[3] = {q, k, v};
-  const int64_t tok[3] = {q_tok, k_tok, v_tok};
-  const int64_t sq[3] = {q_seq, k_seq, v_seq};
-  const char* names[3] = {"q", "k", "v"};
-  uint64_t lo[4], hi[4];
-  for (int i = 0; i < 3; ++i) {
-    if (((uintptr_t)ins[i] & 15u) != 0) return fail(DZ_ERR_INVALID, std::string("attention: ") + names[i] + " is not 16-byte aligned");
-    if (tok[i] < (int64_t)H * head_dim || tok[i] % 8 != 0 || sq[i] < 0 || sq[i] % 8 != 0 || tok[i] > (1LL << 40) ||
-        sq[i] > (1LL << 40)) {
-      return fail(DZ_ERR_INVALID, std::string("attention: strides of ") + names[i] +
-                                      " must be multiples of 8 elements, the token stride at least H * head_dim");
-    }
-    const uint64_t extent = (uint64_t)(n_seq - 1) * (uint64_t)sq[i] + (uint64_t)(L - 1) * (uint64_t)tok[i] +
-                            (uint64_t)H * head_dim;
-    lo[i] = (uint64_t)(uintptr_t)ins[i];
-    hi[i] = lo[i] + extent * 2;
-    int32_t rc = check_range(lo[i], extent * 2, names[i], 0);
-    if (rc) return rc;
-  }
-  if (((uintptr_t)out & 15u) != 0) return fail(DZ_ERR_INVALID, "attention: out is not 16-byte aligned");
-  const uint64_t out_bytes = (uint64_t)n_seq * L * H * head_dim * 2;
-  lo[3] = (uint64_t)(uintptr_t)out;
-  hi[3] = lo[3] + out_bytes;
-  int32_t rc = check_range(lo[3], out_bytes, "out", 0);
-  if (rc) return rc;
-  for (int i = 0; i < 3; ++i) {
-    if (lo[3] < hi[i] && lo[i] < hi[3]) return fail(DZ_ERR_INVALID, std::string("attention: out overlaps ") + names[i]);
-  }
-  dz::AttnArgs a;
-  a.q = (const uint16_t*)q;
-  a.k = (const uint16_t*)k;
-  a.v = (const uint16_t*)v;
-  a.out = (uint16_t*)out;
-  a.q_tok = q_tok;
-  a.k_tok = k_tok;
-  a.v_tok = v_tok;
-  a.q_seq = q_seq;
-  a.k_seq = k_seq;
-  a.v_seq = v_seq;
-  a.L = L;
-  a.H = H;
-  a.scale = scale;
-  hipError_t e = dz::launch_attn_causal(dtype, head_dim, a, (uint32_t)((int64_t)n_seq * H), (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(e, "attention kernel launch");
-  return DZ_OK;
-}
 
 }  // extern "C"

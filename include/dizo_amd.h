@@ -163,6 +163,17 @@ int32_t dz_philox(uint64_t seed, uint32_t stream_id, uint64_t q0, int64_t n, uin
 int32_t dz_group_sumsq(dz_table* t, double* d_sumsq, float* d_norm_f32, void* d_norm_T,
                        void* stream);
 
+/* Set-up of the allocation-free entry point on `device`, which must be the
+ * current device: loads the library's device code there, resolves the
+ * address of its static scratch array and makes one empty kernel launch (the
+ * runtime allocates for a library's first launch on a device), then waits
+ * for it on the null stream. No counterpart in the reference. For
+ * callers that cannot allocate (below): call it once per device before the
+ * first dz_group_sumsq_static on that device, outside any graph capture (the
+ * HIP runtime loads a library's device code on first use, which allocates).
+ * Returns DZ_ERR_DEVICE if `device` is not the current device. */
+int32_t dz_init(int32_t device);
+
 /* dz_group_sumsq without a table and without allocating: no counterpart in
  * the reference. For callers that cannot allocate device memory (code under
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). The n
@@ -173,7 +184,8 @@ int32_t dz_group_sumsq(dz_table* t, double* d_sumsq, float* d_norm_f32, void* d_
  * 4096 groups and 262,144 chunks of 32,768 elements (8.6 G elements); larger
  * inputs return DZ_ERR_INVALID. Every call on one device shares that array,
  * so calls that overlap in time on one device race: order them on one
- * stream. */
+ * stream. After dz_init(device) a call allocates nothing; without it, the
+ * first call on a device does dz_init's work itself. */
 int32_t dz_group_sumsq_static(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const int64_t* numels,
                               int32_t n, int32_t dtype, double* d_sumsq, float* d_norm_f32, void* d_norm_T,
                               void* stream);
@@ -196,24 +208,6 @@ int32_t dz_project(dz_table* t, const void* d_alpha, int32_t mode, double* d_sum
  * (autograd through trainer.py:428-429 in DiZO.forward, trainer.py:714-741). */
 int32_t dz_group_dot(dz_table* t, const uint64_t* other_ptrs, double* d_dot, float* d_dot_f32,
                      void* stream);
-
-/* Causal self-attention of an unpadded batch, for the ZO step's forwards. No
- * counterpart in the reference: it replaces the SDPA call inside HF
- * transformers' OPTAttention.forward when no mask is given (is_causal), a
- * library the reference calls from its model forward. Not bit for bit with
- * SDPA (within its rounding), so the step's loss trajectory drifts from the
- * SDPA one; the trainer uses it only when asked (zo_fused_attention).
- * dtype DZ_DTYPE_F16 or DZ_DTYPE_BF16; head_dim 64 or 128;
- * L a multiple of 32 in [32, 256]. Element offsets: token t of sequence b,
- * head h of q starts at q + b * q_seq + t * q_tok + h * head_dim (k and v
- * alike); pointers and strides 16-byte aligned. q is used as R_T(q * scale)
- * (HF scales q by head_dim^-0.5 in T before the product); softmax and
- * accumulation in fp32, P rounded to T before the product with V. out:
- * (n_seq, L, H, head_dim) contiguous, not overlapping q, k or v. */
-int32_t dz_attention_causal(int32_t dtype, const void* q, const void* k, const void* v, void* out,
-                            int64_t q_tok, int64_t k_tok, int64_t v_tok, int64_t q_seq, int64_t k_seq,
-                            int64_t v_seq, int32_t n_seq, int32_t L, int32_t H, int32_t head_dim, float scale,
-                            void* stream);
 
 #ifdef __cplusplus
 }
