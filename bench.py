@@ -21,10 +21,7 @@ with two GEMM-level fusions that give HF's values bit for bit at the bench
 shapes (fc1 + ReLU as one GEMM with a ReLU epilogue; k/v/q as one GEMM), and
 logits computed only at the option positions the classification loss reads
 (HF's logits_to_keep; the same loss). --full-logits computes them at every
-position as the reference does; --hf-layers runs HF's layer code as it is;
---dz-attention sends an unpadded batch's causal attention through the
-library's MFMA kernel (dz_attention_causal; within SDPA's rounding, not bit
-for bit, so its loss trajectory drifts from SDPA's: opt-in).
+position as the reference does; --hf-layers runs HF's layer code as it is.
 
 Prints one JSON line. `roofline` is the dominant library kernel (the
 multi-tensor perturb / restore+update read-modify-write): algorithmic bytes
@@ -37,7 +34,6 @@ reference's expressions (the oracle's torch restatement) on the host cores:
 the whole step at C1, a sampled and scaled step otherwise.
 
   python bench.py [--gpus 1] [--steps 50] [--warmup 3] [--workload c4] [--graph] [--full-logits] [--hf-layers]
-                  [--dz-attention]
   python bench.py --kernels [--workload c2|c4]  # per-pass kernel microbench (config C2: OPT-2.7B fp16)
 """
 from __future__ import annotations
@@ -99,7 +95,7 @@ def event_offset(steps: int, warmup: int, interval: int = 50) -> int:
 
 
 def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = False, option_head: bool = False,
-              enhanced: str = "zo", fused: bool = False, attention: bool = False, host_grad: bool = False):
+              enhanced: str = "zo", fused: bool = False, host_grad: bool = False):
     import numpy as np
     import torch
 
@@ -120,7 +116,7 @@ def run_steps(wl_name: str, steps: int, warmup: int, log=print, graph: bool = Fa
     offset = event_offset(steps, warmup, DIZO_INTERVAL) if enhanced != "none" else 0
     args = ZOArguments(learning_rate=1e-6, zo_eps=1e-3, max_steps=offset + warmup + steps,
                        enhanced=None if enhanced == "none" else enhanced, zo_graph=graph, zo_option_head=option_head,
-                       zo_fused_mlp=fused, zo_fused_qkv=fused, zo_fused_attention=fused and attention,
+                       zo_fused_mlp=fused, zo_fused_qkv=fused,
                        zo_host_grad=host_grad)
     np.random.seed(26)
     tr = ZOTrainer(model, args, train_dataloader=Cycle(batches), base_model=base)
@@ -173,6 +169,43 @@ def amortised(steps: int, elapsed: float, event_s, interval: int = 50):
         return steps / elapsed, steps / elapsed, None
     mean_ev = t_ev / len(event_s)
     return steps / (t_steps + mean_ev * steps / interval), steps / t_steps, mean_ev
+
+
+ZO_PASSES = ("perturb", "update", "restore_update", "restore_update_perturb")
+
+
+def amortised_passes(summ: dict, steps: int, events: int, P: int, interval: int = 50) -> dict:
+    """Library launches and bytes per ZO parameter per step with one DiZO
+    event per `interval` steps, as `value` amortises the event's time.
+
+    A steady step makes two read-modify-write launches (the -2 perturbation
+    and the fused restore + update + next perturbation). An event adds its
+    projection passes and changes the ZO launches around it (the restore +
+    update before it and the +1 perturbation after it are launches of their
+    own); both are measured in the window per event and spread over
+    `interval` steps. Without events the window's own per-step figures are
+    returned."""
+    zo = [v for k, v in summ.items() if k in ZO_PASSES]
+    ev = [v for k, v in summ.items() if k not in ZO_PASSES]
+    zo_launches = sum(v["launches"] for v in zo)
+    zo_bytes = sum(v["bytes_per_launch"] * v["launches"] for v in zo)
+    if not events:
+        return {"bytes_per_param_per_step": (zo_bytes + sum(v["bytes_per_launch"] * v["launches"] for v in ev))
+                / (steps * P),
+                "library_launches_per_step": (zo_launches + sum(v["launches"] for v in ev)) / steps,
+                "event_amortisation": None}
+    steady = summ.get("restore_update_perturb") or summ.get("perturb")
+    pass_bytes = steady["bytes_per_launch"]
+    zo_extra_launches = (zo_launches - 2 * steps) / events
+    zo_extra_bytes = (zo_bytes - 2 * steps * pass_bytes) / events
+    ev_launches = sum(v["launches"] for v in ev) / events
+    ev_bytes = sum(v["bytes_per_launch"] * v["launches"] for v in ev) / events
+    return {
+        "bytes_per_param_per_step": (2 * pass_bytes + (zo_extra_bytes + ev_bytes) / interval) / P,
+        "library_launches_per_step": 2 + (zo_extra_launches + ev_launches) / interval,
+        "event_amortisation": {"interval_steps": interval, "launches_per_event": ev_launches + zo_extra_launches,
+                               "bytes_per_event": ev_bytes + zo_extra_bytes},
+    }
 
 
 def _cpu_threads() -> int:
@@ -339,7 +372,9 @@ def cpu_baseline_c1(log=print) -> dict:
 
 def cpu_baseline_sampled(wl_name: str, log=print) -> dict:
     """The reference's step on the host cores, estimated from timed samples
-    (the whole C3-C5 step takes minutes on the CPU):
+    (the whole C3-C5 step takes minutes on the CPU; the line labels the
+    result "estimate" and carries the measured passes, GB/s of the sample,
+    beside it):
       * the four ZO passes (trainer.py:1438-1442 x3, 1603-1608; torch.normal
         z, model dtype) over one decoder layer's k_proj and v_proj weights,
         scaled to the whole trainable set by parameter count;
@@ -390,6 +425,8 @@ def cpu_baseline_sampled(wl_name: str, log=print) -> dict:
         t_head = time.perf_counter() - t0
     fwd_per_step = 2 + 20 / 50
     step_s = t_zo + Lyr * t_fwd2 / 2 * fwd_per_step + t_head * fwd_per_step + t_event_proj / 50
+    eb = ws[0].element_size()
+    measured = {k: {"s": v, "GBps": _PASS_BYTES[k] * eb * n_kv / v / 1e9} for k, v in t.items()}
     log(f"[cpu] {wl_name}: ZO passes {t_zo:.1f}s (sampled {n_kv} of {P} params), layer forwards x2 "
         f"{t_fwd2:.2f}s, LM head {t_head:.2f}s, event projection {t_event_proj:.1f}s per event; "
         f"{step_s:.1f}s per step on {cores} threads")
@@ -397,7 +434,9 @@ def cpu_baseline_sampled(wl_name: str, log=print) -> dict:
         "value": 1.0 / step_s,
         "unit": "steps/s",
         "cores": cores,
-        "kind": "port",
+        # an extrapolation from the measured samples below, not a measured step
+        "kind": "estimate",
+        "measured_passes": measured,
         "sample": (f"estimated from timed samples: the 4 ZO passes ({wl['dtype']}, torch.normal z) over one "
                    f"{shape.name} layer's k/v weights ({n_kv} params) scaled to P={P}; 2 forwards of one decoder "
                    f"layer ({rows}x{seq} tokens, fp32) x {Lyr} layers; the full-logit LM head (fp32); the DiZO "
@@ -489,34 +528,6 @@ def kernel_microbench(wl_name: str, reps: int = 10, log=print):
         log(f"[kernels] {name:15s} {t:8.3f} ms {nb / t / 1e6:8.1f} GB/s")
     ptab.close()
     del t0
-    # the forward's causal attention kernel at the workload's batch shape (unpadded batches only): q, k, v
-    # as the fused k/v/q GEMM leaves them; algorithmic bytes = q, k, v read + output written
-    from dizo_amd.attention import attention_causal, supported
-
-    shape = SHAPES[wl["shape"]]
-    hd = shape.d_model // shape.heads
-    Lq = wl["fixed_len"]
-    if Lq:
-        n_seq, d = 2 * wl["batch"], shape.d_model
-        kvq = torch.randn(n_seq, Lq, 3 * d, device="cuda", dtype=torch.float32).to(dtype)
-        k, v, q = kvq.split(d, dim=-1)
-        if supported(q, Lq, hd):
-            fn = lambda: attention_causal(q, k, v, shape.heads, hd, hd ** -0.5)  # noqa: E731
-            fn()
-            torch.cuda.synchronize()
-            ms = []
-            for _ in range(reps):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
-                fn()
-                e1.record()
-                torch.cuda.synchronize()
-                ms.append(e0.elapsed_time(e1))
-            t = float(np.median(ms))
-            nb = 4 * n_seq * Lq * d * kvq.element_size()
-            out["attention"] = {"ms": t, "GBps": nb / t / 1e6, "frac": nb / t / 1e6 / HBM_PEAK_GBPS, "bytes": nb}
-            log(f"[kernels] {'attention':15s} {t:8.3f} ms {nb / t / 1e6:8.1f} GB/s")
-        del kvq, k, v, q
     # calibration for counter-based traffic: a plain device copy of known size
     # (reads and writes copy_bytes each), launched twice
     copy_bytes = 4 << 30
@@ -564,10 +575,6 @@ def main(argv=None):
     ap.add_argument("--hf-layers", action="store_true",
                     help="run HF's decoder layer code as it is (default: fc1 + ReLU as one GEMM with a ReLU "
                          "epilogue, k/v/q as one GEMM; the same values at the bench shapes)")
-    ap.add_argument("--dz-attention", action="store_true",
-                    help="with the fused layers, run an unpadded batch's causal attention through the library's "
-                         "MFMA kernel (within SDPA's rounding, not bit for bit; default: SDPA)")
-    ap.add_argument("--sdpa", action="store_true", help="SDPA's attention (the default; kept for old command lines)")
     ap.add_argument("--host-grad", action="store_true",
                     help="read projected_grad back to the host in every step, as the reference does (default: the "
                          "kernels read it on the device and the step has no synchronisation; the same values)")
@@ -602,9 +609,8 @@ def main(argv=None):
                 line["cpu_baseline"] = {"error": f"{type(e).__name__}: {e}"}
         print(json.dumps(line), flush=True)
         return 0
-    use_dz_attention = a.dz_attention and not a.hf_layers and not a.sdpa
     r = run_steps(a.workload, a.steps, a.warmup, log=log, graph=a.graph, option_head=not a.full_logits,
-                  enhanced=a.enhanced, fused=not a.hf_layers, attention=use_dz_attention, host_grad=a.host_grad)
+                  enhanced=a.enhanced, fused=not a.hf_layers, host_grad=a.host_grad)
     wl = WORKLOADS[a.workload]
     value, zo_rate, event_s = amortised(a.steps, r["elapsed"], r["event_s"])
     summ = r["summary"]
@@ -636,7 +642,7 @@ def main(argv=None):
                    "zo_params": r["P"], "dizo_events_timed": r["events"], "global_batch": 2 * wl["batch"],
                    "first_global_step": r["offset"],
                    "graph": a.graph, "option_head": not a.full_logits, "fused_gemms": not a.hf_layers,
-                   "attention": "dz_attention_causal (unpadded batches)" if use_dz_attention else "sdpa",
+                   "attention": "sdpa",
                    "enhanced": a.enhanced, "projected_grad": "host (.item())" if a.host_grad else "device",
                    "seq_len": wl["fixed_len"] or wl["max_len"],
                    "device": {"name": torch.cuda.get_device_name(0),
@@ -663,11 +669,9 @@ def main(argv=None):
             "rmw_all": {"GBps": rmw_bytes / (rmw_ms * 1e-3) / 1e9 if rmw_ms else None,
                         "frac": rmw_bytes / (rmw_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS if rmw_ms else None,
                         "launches_per_step": rmw_launches / a.steps},
-            # every library pass of the timed region (ZO passes and the DiZO
-            # event's projection passes), per ZO parameter and per step
-            "bytes_per_param_per_step": sum(v["bytes_per_launch"] * v["launches"] for v in summ.values())
-            / (a.steps * r["P"]),
-            "library_launches_per_step": sum(v["launches"] for v in summ.values()) / a.steps,
+            # every library pass, per ZO parameter and per step, with the DiZO
+            # event amortised one per 50 steps as in `value` (amortised_passes)
+            **amortised_passes(summ, a.steps, r["events"], r["P"]),
         },
         "kernels": summ,
         "loss_first_last": [r["losses"][0], r["losses"][-1]] if r["losses"] else None,

@@ -39,7 +39,7 @@ def test_flags_and_workloads():
     assert bench.WORKLOADS["c2"]["kernels_only"] and bench.WORKLOADS["c2"]["shape"] == "opt-2.7b"
     c4 = bench.WORKLOADS["c4"]
     assert (c4["shape"], c4["dtype"], c4["batch"], c4["fixed_len"]) == ("opt-13b", "float16", 16, 128)
-    for flags in (["--graph"], ["--full-logits"], ["--hf-layers"], ["--sdpa"], ["--dz-attention"], ["--kernels"],
+    for flags in (["--graph"], ["--full-logits"], ["--hf-layers"], ["--kernels"],
                   ["--enhanced", "fo"],
                   ["--workload", "c5"], ["--workload", "c2", "--kernels"], ["--no-cpu-baseline"]):
         assert bench.main(flags + ["--gpus", "3"]) == 2  # parses, then stops at the one-GPU check
@@ -64,3 +64,29 @@ def test_amortised_rate():
     v, _, _ = bench.amortised(50, 10.0, [2.0])
     assert abs(v - 5.0) < 1e-12
     assert bench.amortised(10, 2.0, []) == (5.0, 5.0, None)
+
+
+def test_amortised_passes_spread_the_event_over_fifty_steps():
+    # the window of a 20-step run with the event on its last step (C4 fp16):
+    # 20 x -2, 19 three-way, 1 restore+update before the event, 1 +1 after it;
+    # the event's 1 sumsq, 21 apply and 20 reverse+norm passes
+    P, b, kv = 12_596_080_640, 50_384_322_560.0, 2_097_152_000
+    summ = {"perturb": {"launches": 21, "bytes_per_launch": b},
+            "restore_update_perturb": {"launches": 19, "bytes_per_launch": b},
+            "restore_update": {"launches": 1, "bytes_per_launch": b},
+            "proj_sumsq": {"launches": 1, "bytes_per_launch": 4.0 * kv},
+            "proj_apply": {"launches": 21, "bytes_per_launch": 6.0 * kv},
+            "proj_reverse_sumsq": {"launches": 20, "bytes_per_launch": 6.0 * kv}}
+    got = bench.amortised_passes(summ, 20, 1, P)
+    # per 50 steps: 101 RMW launches (2 per step and 1 around the event) and 42 projection launches
+    assert abs(got["library_launches_per_step"] - (101 + 42) / 50) < 1e-12
+    want = (101 * b + (4 + 41 * 6) * kv) / 50 / P
+    assert abs(got["bytes_per_param_per_step"] - want) < 1e-12
+    # the same window read over more steps gives the same amortised figures
+    summ2 = dict(summ, perturb={"launches": 51, "bytes_per_launch": b},
+                 restore_update_perturb={"launches": 49, "bytes_per_launch": b})
+    got2 = bench.amortised_passes(summ2, 50, 1, P)
+    assert abs(got2["library_launches_per_step"] - got["library_launches_per_step"]) < 1e-12
+    # without events: the window's own figures
+    none = bench.amortised_passes({"perturb": {"launches": 10, "bytes_per_launch": b}}, 5, 0, P)
+    assert none["library_launches_per_step"] == 2 and none["event_amortisation"] is None
