@@ -167,15 +167,14 @@ def dizo_zo_iteration(news, anchors, gammas: list, init: bool, z_gamma: Sequence
     return ts, loss1, loss2
 
 
-def forward_loss(model, input_ids, attention_mask, labels, option_len, num_options, pad_id: int) -> torch.Tensor:
-    """trainer.py:1446-1522 (classification branch) with torch ops: the full
-    logits, the per-row option masking loop and the option-position
-    log-probability mean, then the cross-entropy over each example's
-    candidates. The CPU baseline's forward and loss."""
+def option_loss(logits, input_ids, labels, option_len, num_options, pad_id: int) -> torch.Tensor:
+    """trainer.py:495-528 (the classification branch of
+    forward_wrap_with_option_len, also trainer.py:1466-1508) on given logits:
+    shift, the per-row option masking loop, log_softmax over the vocabulary,
+    the option-position log-probability mean, then the cross-entropy over
+    each example's candidates."""
     import torch.nn.functional as F
 
-    with torch.no_grad():
-        logits = model(input_ids=input_ids, attention_mask=attention_mask).logits
     shift_logits = logits[..., :-1, :].contiguous()
     shift_labels = torch.clone(input_ids)[..., 1:].contiguous()
     shift_labels[shift_labels == pad_id] = -100
@@ -197,6 +196,96 @@ def forward_loss(model, input_ids, attention_mask, labels, option_len, num_optio
             start = end
         return loss / count
     return loss_fct(selected.view(-1, nopt[0]), labels.view(-1, nopt[0])[:, 0])
+
+
+def forward_loss(model, input_ids, attention_mask, labels, option_len, num_options, pad_id: int) -> torch.Tensor:
+    """trainer.py:1446-1522 (classification branch) with torch ops: the full
+    logits of a forward without gradients, then option_loss. The CPU
+    baseline's forward and loss."""
+    with torch.no_grad():
+        logits = model(input_ids=input_ids, attention_mask=attention_mask).logits
+    return option_loss(logits, input_ids, labels, option_len, num_options, pad_id)
+
+
+def forward_wrap_with_option_len(model, input_ids=None, labels=None, option_len=None, num_options=None,
+                                 **kwargs) -> torch.Tensor:
+    """DiZO.forward_wrap_with_option_len, trainer.py:470-542 (classification
+    branch), as the first-order DiZO path calls it: the model's forward with
+    autograd enabled (full logits), then option_loss with the model's own pad
+    id (trainer.py:501). Returns the loss."""
+    logits = model(input_ids=input_ids, **kwargs).logits
+    return option_loss(logits, input_ids, labels, option_len, num_options, model.config.pad_token_id)
+
+
+def dizo_fo_objective(model, anchors: dict, names: Sequence[str], gammas: Sequence[torch.Tensor], data: dict):
+    """DiZO.forward with apply=False, trainer.py:714-741: a deep copy of the
+    model in eval mode, apply_constraints on it (trainer.py:405-436, every
+    parameter's requires_grad cleared, alpha = gamma / (torch.norm(Delta) +
+    1e-8) per projected tensor, the copy_ recorded by autograd), the loss of
+    forward_wrap_with_option_len and 1e-3 * sum |gamma|.
+
+    anchors: name -> theta0 tensor; names: the projected tensors in the order
+    of the gamma Parameters. Returns (pgm_loss, vs, deltas, denominators): the
+    differentiable v = Delta * alpha of each group (retain_grad() set) and
+    its Delta and norm + 1e-8, for the gradient bound of a test (v.grad is
+    kept when gamma requires a gradient)."""
+    import copy
+
+    cm = copy.deepcopy(model)
+    cm.eval()
+    for p in cm.parameters():
+        p.requires_grad = False
+    named = dict(cm.named_parameters())
+    vs, deltas, denoms = [], [], []
+    for g, n in zip(gammas, names):
+        new_para, anchor_para = named[n], anchors[n]
+        t = new_para.detach() - anchor_para.detach()
+        denom = torch.norm(t) + 1e-8
+        alpha = g / denom
+        v = (new_para.detach() - anchor_para.detach()) * alpha
+        if v.requires_grad:
+            v.retain_grad()
+        temp = v + anchor_para.detach()
+        new_para.copy_(temp)
+        vs.append(v)
+        deltas.append(t)
+        denoms.append(denom.detach())
+    loss = forward_wrap_with_option_len(cm, **data)
+    pgm_loss = loss + 1e-3 * sum(p.abs().sum() for p in gammas)
+    return pgm_loss, vs, deltas, denoms
+
+
+def dizo_fo_apply(model, anchors: dict, names: Sequence[str], gammas: Sequence[torch.Tensor]) -> None:
+    """DiZO.forward with apply=True, trainer.py:720-725 (apply_constraints in
+    place under no_grad, trainer.py:428-433)."""
+    named = dict(model.named_parameters())
+    with torch.no_grad():
+        for g, n in zip(gammas, names):
+            new_para, anchor_para = named[n], anchors[n]
+            alpha = g / (torch.norm(new_para.detach() - anchor_para.detach()) + 1e-8)
+            temp = (new_para.detach() - anchor_para.detach()) * alpha + anchor_para.detach()
+            new_para.copy_(temp)
+
+
+def dizo_fo_event(model, anchors: dict, names: Sequence[str], batches: Sequence[dict], max_iters: int = 10,
+                  proj_lr: float = 0.1):
+    """dizo_trainer.dizo_iters, trainer.py:805-830: one fp32 gamma Parameter
+    per projected tensor, created as torch.Tensor([0]) (trainer.py:388-403),
+    Adam(lr = proj_lr) (trainer.py:758), max_iters iterations of the
+    objective, backward and step, each on the next batch, then the final
+    apply. Returns (gammas as one fp32 tensor, the iterations' losses)."""
+    dev = next(model.parameters()).device
+    gammas = [torch.nn.Parameter(torch.Tensor([0]).to(dev)) for _ in names]
+    opt = torch.optim.Adam(gammas, lr=proj_lr)
+    losses = []
+    for it in range(max_iters):
+        pgm, _, _, _ = dizo_fo_objective(model, anchors, names, gammas, batches[it % len(batches)])
+        losses.append(float(pgm.detach()))
+        opt.zero_grad()
+        pgm.backward()
+        opt.step()
+    dizo_fo_apply(model, anchors, names, gammas)
+    return torch.cat([g.detach().reshape(1) for g in gammas]), losses
 
 
 def zo_step_sampled(model, params: Sequence[torch.Tensor], batch: dict, seed: int, zo_eps: float,

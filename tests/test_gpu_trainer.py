@@ -180,58 +180,34 @@ def _ulp_diff(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return (ia - ib).abs()
 
 
-def _ref_fo_event(model, anchor, names, batches, exact_dot: bool):
-    """The reference's first-order event (trainer.py:714-741, 805-830) written
-    with torch: per iteration a deep copy of the model, apply_constraints with
-    autograd through alpha = gamma / (||Delta|| + 1e-8), the DiZO loss forward,
-    the L1 term, backward and Adam(lr 0.1); then the final apply in place.
-    exact_dot forms v = Delta * alpha through fp64 (the same fp32 values: the
-    product of an fp16/bf16/fp32 Delta and an fp32 alpha is exact in fp64), so
-    autograd's sum(grad * Delta) accumulates in fp64 as the library's kernel
-    does; without it torch sums in fp32."""
-    from dizo_amd.trainer import option_len_loss
-    G = len(names)
-    gammas = [torch.nn.Parameter(torch.Tensor([0]).cuda()) for _ in range(G)]
-    opt = torch.optim.Adam(gammas, lr=0.1)
-    a_b = dict(anchor.named_parameters())
-    losses = []
-    for it in range(10):
-        data = batches[it % len(batches)]
-        cm = copy.deepcopy(model)
-        cm.eval()
-        for p in cm.parameters():
-            p.requires_grad = False
-        named = dict(cm.named_parameters())
-        for i, n in enumerate(names):
-            newp, a = named[n], a_b[n]
-            alpha = gammas[i] / (_lib_norm(newp.detach() - a.detach()) + 1e-8)
-            delta = newp.detach() - a.detach()
-            v = (delta.double() * alpha.double()).float() if exact_dot else delta * alpha
-            newp.copy_(v + a.detach())
-        loss = option_len_loss(cm, True, **data, return_dict=True).loss
-        losses.append(float(loss))
-        pgm = loss + 1e-3 * sum(g.abs().sum() for g in gammas)
-        opt.zero_grad()
-        pgm.backward()
-        opt.step()
-    pb = dict(model.named_parameters())
-    with torch.no_grad():
-        for i, n in enumerate(names):
-            newp, a = pb[n], a_b[n]
-            alpha = gammas[i] / (_lib_norm(newp - a) + 1e-8)
-            newp.copy_((newp - a) * alpha + a)
-    return torch.cat([g.detach().reshape(1) for g in gammas]), losses
+def _lib_group_norms(params, anchors) -> torch.Tensor:
+    """The library's norms of theta - theta0 per group (product side: the
+    projection table's norm pass), in the model dtype."""
+    from dizo_amd.table import ProjTable
+    tab = ProjTable(params, anchors)
+    out = torch.empty(len(params), dtype=params[0].dtype, device=params[0].device)
+    tab.group_sumsq(norm_T=out)
+    torch.cuda.synchronize()
+    tab.close()
+    return out
 
 
 @pytest.mark.parametrize("dt", DTS)
 def test_dizo_first_order_event_matches_reference(dt):
     """ENHANCED=fo: dizo_trainer.dizo_iters (10 Adam steps on fp32 gamma through
-    autograd, then the final apply) against the reference's procedure written
-    with torch and its alpha-gradient accumulated in fp64 like the kernel's:
-    gamma to 1e-5 relative, every tensor within one unit in the last place,
-    non-projected tensors untouched. torch's own fp32 accumulation of that
-    heavily cancelling sum moves gamma by up to ~1% after 10 Adam steps; that
-    run is checked at 5%."""
+    autograd, then the final apply) against the reference's procedure as it is
+    written (oracle.ref_torch.dizo_fo_event: trainer.py:714-741, 805-830, a
+    deep copy per iteration, torch.norm, the reference's loss, torch's fp32
+    autograd), each run freely from gamma = 0.
+
+    The gammas agree within 5 % (the measured difference is printed): the
+    alpha-gradient is a heavily cancelling sum, which the reference's autograd
+    accumulates in fp32 in torch's order and the library in fp64, and Adam
+    normalises each step, so summation rounding moves gamma by a fraction of a
+    step (test_dizo_first_order_iterations_within_the_fp32_sum_bound bounds
+    the per-iteration difference). Every tensor is within one unit in the
+    last place of the reference's final apply made with the library's gamma,
+    and the non-projected tensors are untouched."""
     from dizo_amd.dizo import dizo_trainer
     from dizo_amd.synth import Cycle
     from dizo_amd.trainer import select_trainable
@@ -252,47 +228,52 @@ def test_dizo_first_order_event_matches_reference(dt):
     g_lib = dtr.dizo.gamma().detach()
     assert g_lib.dtype == torch.float32
 
-    g_ref, _ = _ref_fo_event(model_b, anchor_b, names, batches, exact_dot=True)
-    assert torch.allclose(g_lib, g_ref, rtol=1e-5, atol=1e-7), f"gamma {g_lib} vs {g_ref}"
-    pa, pb = dict(model_a.named_parameters()), dict(model_b.named_parameters())
-    for n in pb:
-        d = _ulp_diff(pa[n].data, pb[n].data)
+    anchors = dict(anchor_b.named_parameters())
+    g_ref, _ = R.dizo_fo_event(model_b, anchors, names, batches)
+    rel = float(((g_lib - g_ref).abs() / g_ref.abs().clamp_min(1e-6)).max())
+    print(f"{dt}: largest relative gamma difference against the reference's fp32 autograd: {rel:.3g}", flush=True)
+    assert torch.allclose(g_lib, g_ref, rtol=5e-2, atol=1e-4), f"gamma {g_lib} vs {g_ref}"
+
+    R.dizo_fo_apply(model_c, anchors, names, [g_lib[i:i + 1] for i in range(len(names))])
+    pa, pc = dict(model_a.named_parameters()), dict(model_c.named_parameters())
+    for n in pc:
+        d = _ulp_diff(pa[n].data, pc[n].data)
         assert int(d.max()) <= 1, f"{n}: {int(d.max())} ulp"
         if n not in names:
-            assert torch.equal(_bits(pa[n].data), _bits(pb[n].data)), f"{n} changed"
-
-    g_torch, _ = _ref_fo_event(model_c, copy.deepcopy(anchor_b), names, batches, exact_dot=False)
-    assert torch.allclose(g_lib, g_torch, rtol=5e-2, atol=1e-4), f"gamma {g_lib} vs torch fp32 {g_torch}"
+            assert torch.equal(_bits(pa[n].data), _bits(pc[n].data)), f"{n} changed"
     dtr.close()
 
 
 @pytest.mark.parametrize("dt", DTS)
 def test_dizo_first_order_iterations_within_the_fp32_sum_bound(dt):
     """ENHANCED=fo, iteration by iteration against the reference's procedure as
-    it is written (trainer.py:714-741, 805-830: a deep copy, apply_constraints
-    with autograd through alpha = gamma / (||Delta|| + 1e-8), the loss plus
-    1e-3 * sum|gamma|, backward), each iteration started from the library's
-    gamma of that iteration:
+    it is written (oracle.ref_torch.dizo_fo_objective: trainer.py:714-741, a
+    deep copy, apply_constraints with autograd through alpha = gamma /
+    (torch.norm(Delta) + 1e-8), the reference's loss, 1e-3 * sum|gamma|,
+    backward), each iteration started from the library's gamma of that
+    iteration:
 
-    * the objective agrees within north_star's 1e-3 (the projected weights are
-      the same, so the forwards are too);
-    * the gradient with respect to each gamma differs only by how the
-      reference's autograd sums g_j = dL/dtheta'_j * Delta_j over the group:
-      torch adds the fp32 products in fp32, in some order, the library in
-      fp64. Any fp32 summation order is within (n - 1) u sum|g_j| of the exact
-      sum (u = 2^-24; the fp16 / bf16 products are exact in fp32, an fp32
-      product adds u |g_j|), and the test asserts that bound, divided by the
-      norm as the reference divides, plus four units in the last place;
+    * the objective agrees within north_star's 1e-3;
+    * the gradient with respect to each gamma is S / d: S = sum_j
+      dL/dtheta'_j * Delta_j over the group, d = norm + 1e-8. The two sides
+      differ in how they sum S (the reference's autograd adds the fp32
+      products in fp32, in some order; the library in fp64: any fp32
+      summation order is within (n - 1) u sum|g_j| of the exact sum, u =
+      2^-24; the fp16 / bf16 products are exact in fp32, an fp32 product adds
+      u |g_j|) and in d (torch.norm accumulates in fp32, the library in fp64;
+      both round to the model dtype and may land one unit apart). The test
+      asserts |g_ref - g_lib| <= (n - 1) u sum|g_j| / d_ref + |g_lib| |d_lib /
+      d_ref - 1| + four units in the last place;
     * after the ten Adam steps the final apply with the library's gamma gives
       every tensor within one unit in the last place of the reference's.
 
-    The two gamma trajectories, each run freely, drift apart by up to about 1 %
+    The two gamma trajectories, each run freely, drift apart by about 1 %
     over the ten Adam steps (test_dizo_first_order_event_matches_reference):
     the sum cancels heavily and Adam normalises the step, so summation
     rounding moves gamma by a step's fraction."""
     from dizo_amd.dizo import dizo_trainer
     from dizo_amd.synth import Cycle
-    from dizo_amd.trainer import option_len_loss, select_trainable
+    from dizo_amd.trainer import select_trainable
     model_a, model_b, batches = _setup(dt, seed=23)
     anchor = copy.deepcopy(model_a)  # theta0; theta = theta0 + noise
     gen = torch.Generator(device="cuda").manual_seed(4)
@@ -306,7 +287,9 @@ def test_dizo_first_order_iterations_within_the_fp32_sum_bound(dt):
     dz = dtr.dizo
     names = dz.constraints_name
     G = len(names)
-    a_b = dict(anchor.named_parameters())
+    anchors = dict(anchor.named_parameters())
+    pa0 = dict(model_a.named_parameters())
+    d_lib = _lib_group_norms([pa0[n].data for n in names], [anchors[n].data for n in names]).float()
     u = 2.0 ** -24
     worst = loosest = 0.0
     for it in range(10):
@@ -319,32 +302,17 @@ def test_dizo_first_order_iterations_within_the_fp32_sum_bound(dt):
         dtr.pgm_optimizer.step()
         dz.fo_restore()
 
-        cm = copy.deepcopy(model_b)
-        cm.eval()
-        for p in cm.parameters():
-            p.requires_grad = False
-        named = dict(cm.named_parameters())
         gam = [torch.nn.Parameter(gamma_t[i:i + 1].clone()) for i in range(G)]
-        vs, deltas, denoms = [], [], []
-        for i, n in enumerate(names):
-            newp, a = named[n], a_b[n]
-            denom = _lib_norm(newp.detach() - a.detach()) + 1e-8
-            delta = newp.detach() - a.detach()
-            v = delta * (gam[i] / denom)
-            v.retain_grad()
-            newp.copy_(v + a.detach())
-            vs.append(v)
-            deltas.append(delta)
-            denoms.append(float(denom))
-        loss = option_len_loss(cm, True, **data, return_dict=True).loss
-        pgm_ref = loss + 1e-3 * sum(g.abs().sum() for g in gam)
+        pgm_ref, vs, deltas, denoms = R.dizo_fo_objective(model_b, anchors, names, gam, data)
         assert abs(float(pgm_ref) - float(pgm)) <= 1e-3, (it, float(pgm_ref), float(pgm))
         pgm_ref.backward()
         g_ref = torch.cat([g.grad.reshape(1) for g in gam]).detach()
         for i in range(G):
             prod = vs[i].grad.double() * deltas[i].double()
             n_terms = prod.numel()
-            bound = (n_terms * u * float(prod.abs().sum()) / (1 - n_terms * u)) / denoms[i] \
+            d_ref = float(denoms[i])
+            norm_term = abs(float(g_lib[i])) * abs(float(d_lib[i]) + 1e-8 - d_ref) / d_ref
+            bound = (n_terms * u * float(prod.abs().sum()) / (1 - n_terms * u)) / d_ref + norm_term \
                 + 4 * u * max(abs(float(g_lib[i])), abs(float(g_ref[i]))) + 1e-30
             diff = abs(float(g_ref[i]) - float(g_lib[i]))
             assert diff <= bound, f"iteration {it} group {i}: |{float(g_ref[i])} - {float(g_lib[i])}| > {bound}"
@@ -352,17 +320,12 @@ def test_dizo_first_order_iterations_within_the_fp32_sum_bound(dt):
             loosest = max(loosest, bound / max(abs(float(g_lib[i])), 1e-30))
     dz(model_a, dtr.pre_trained, apply=True)  # trainer.py:830
     g_fin = dz.gamma().detach()
-    pb = dict(model_b.named_parameters())
-    with torch.no_grad():
-        for i, n in enumerate(names):
-            newp, a = pb[n], a_b[n]
-            alpha = g_fin[i:i + 1] / (_lib_norm(newp - a) + 1e-8)
-            newp.copy_((newp - a) * alpha + a)
-    pa = dict(model_a.named_parameters())
+    R.dizo_fo_apply(model_b, anchors, names, [g_fin[i:i + 1] for i in range(G)])
+    pa, pb = dict(model_a.named_parameters()), dict(model_b.named_parameters())
     for n in pb:
         d = _ulp_diff(pa[n].data, pb[n].data)
         assert int(d.max()) <= 1, f"{n}: {int(d.max())} ulp"
-    print(f"largest gradient difference: {worst:.3g} of the fp32 summation bound; "
+    print(f"largest gradient difference: {worst:.3g} of the bound; "
           f"largest bound: {loosest:.3g} of the gradient", flush=True)
     dtr.close()
 
