@@ -387,18 +387,103 @@ def test_c5_two_whole_steps_bit_exact():
     tr.zo_close()
 
 
+def test_c5_dizo_event_bit_exact(capsys):
+    """Config C5 (OPT-30B bf16, 771 tensors, batch 8 x 2 x 256) with its DiZO
+    event: the library trainer started at global step 48, so the event
+    (trainer.py:1611-1615, 782-803: 10 SPSA iterations on the 96 k/v gammas
+    with 20 forwards, then the final apply) follows the update of the second
+    step; against the reference's expressions in the recipe form fed the
+    exported z one tensor at a time, the exported gamma noise and the
+    library's norm definition: the two losses, the 96 gammas and all 771
+    tensors bit for bit."""
+    from dizo_amd import _lib as L
+    from dizo_amd.synth import Cycle, build_opt, make_batches
+    from dizo_amd.table import normals
+    from dizo_amd.trainer import ZOArguments, ZOTrainer, select_trainable
+    report = _reporter(capsys)
+    dt, lr0, eps, steps = torch.bfloat16, 1e-6, 1e-3, 2
+    batches = make_batches(3, 8, 50272, seed=17, device="cuda", fixed_len=256)
+    model = build_opt("opt-30b", dt, "cuda", seed=0)
+    init = copy.deepcopy(model)  # becomes the reference side
+    args = ZOArguments(learning_rate=lr0, zo_eps=eps, max_steps=100, enhanced="zo")
+    np.random.seed(26)
+    tr = ZOTrainer(model, args, train_dataloader=Cycle(batches))
+    tr.state.global_step = 48  # the event follows the update of global step 49
+    proj = tr.dizo_trainer.dizo.constraints_name
+    G = len(proj)
+    assert G == 96
+    p_init = dict(init.named_parameters())
+    anchors = [p_init[n].detach().clone() for n in proj]  # theta0 of the projected tensors
+    la, lrs = [], []
+    for k in range(steps):
+        lrs.append(float(tr._get_learning_rate()))
+        la.append(tr.training_step(batches[k]).reshape(()).clone())
+        report("library c5", k, steps)
+    tr.zo_flush()
+    torch.cuda.synchronize()
+    assert tr.dizo_trainer.i == 1, "the DiZO event did not run"
+    g_lib = tr.dizo_trainer.dizo.gamma().detach().clone()
+
+    named, _ = select_trainable(init)
+    assert len(named) == 771
+    names = [n for n, _ in named]
+    params = [p for _, p in named]
+    np.random.seed(26)
+
+    def each(op, seed, *a):
+        for n, p in zip(names, params):
+            z = tr.export_z(n, seed)
+            op([p], [z], *a)
+            del z
+
+    lb = []
+    for k in range(steps):
+        seed = np.random.randint(1000000000)
+        batch = batches[k]
+        each(R.zo_perturb_parameters_recipe, seed, 1, eps)
+        l1 = _ref_forward(init, batch)
+        each(R.zo_perturb_parameters_recipe, seed, -2, eps)
+        l2 = _ref_forward(init, batch)
+        g = R.projected_grad(l1, l2, eps)
+        each(R.zo_perturb_parameters_recipe, seed, 1, eps)
+        each(R.zo_update_recipe, seed, g, lrs[k])
+        lb.append(l1)
+        report("reference c5", k, steps)
+    # the event after the second step's update, with that step's seed for the gamma noise
+    news = [p_init[n] for n in proj]
+    gammas = [torch.nn.Parameter(torch.Tensor([0]).cuda()) for _ in range(G)]
+    pgm = iter(Cycle(batches))
+    dev = torch.device("cuda", 0)
+    for it in range(10):
+        zg = normals(seed, L.DZ_STREAM_GAMMA, it * G, G, dt, dev)
+        data = next(pgm)
+        R.dizo_zo_iteration(news, anchors, gammas, it == 0, [zg[i:i + 1] for i in range(G)],
+                            lambda j: _ref_forward(init, data), norm=_lib_norm)
+        report("reference c5 event", it, 10)
+    R.apply_constraints(news, anchors, gammas, norm=_lib_norm)
+    torch.cuda.synchronize()
+    g_ref = torch.cat([g.detach().reshape(1) for g in gammas])
+    print("C5 losses:", [float(x) for x in la], flush=True)
+    bad = [k for k, (a, b) in enumerate(zip(la, lb)) if not _same(a, b)]
+    assert not bad, f"losses differ at steps {bad}: {[(float(la[k]), float(lb[k])) for k in bad]}"
+    assert _same(g_lib.to(g_ref.dtype), g_ref), f"gamma: {int((_bits(g_lib) != _bits(g_ref)).sum())} of {G} differ"
+    pm = dict(model.named_parameters())
+    diff = [n for n in names if not _same(pm[n].data, p_init[n].data)]
+    assert not diff, f"{len(diff)} tensors differ after the event, e.g. {diff[:3]}"
+    tr.zo_close()
+
+
 def test_c3_shape_fused_forward_bit_identical():
     """The bench's forward at C3's shape (OPT-2.7B fp16, padded batches of 16 x 2
-    candidates): with the fused decoder-layer GEMMs and the library attention
-    asked for (padded batches keep SDPA), 50 steps with a DiZO event give the
-    losses, gamma and weights of HF's layer code bit for bit."""
+    candidates): with the fused decoder-layer GEMMs, 50 steps with a DiZO event
+    give the losses, gamma and weights of HF's layer code bit for bit."""
     from dizo_amd.synth import make_batches
 
     batches = make_batches(8, 16, 50272, seed=3, device="cuda", min_len=32, max_len=64)
     runs = []
     for fused in (True, False):
         tr, la, ma, _ = _library_run("opt-2.7b", torch.float16, batches, 50, 1e-6, 1e-3, zo_fused_mlp=fused,
-                                     zo_fused_qkv=fused, zo_fused_attention=fused, zo_option_head=True)
+                                     zo_fused_qkv=fused, zo_option_head=True)
         runs.append((tr.dizo_trainer.dizo.gamma(), la, {n: p.detach().clone() for n, p in ma.named_parameters()}))
         tr.zo_close()
         del tr, ma

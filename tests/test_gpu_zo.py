@@ -319,12 +319,16 @@ def test_update_rounds_ties_like_torch_cpu_and_cuda():
     * The library's update rounds the fp32 product to even, as torch on the
       CPU does (and CUDA, whose opmath kernels compute in fp32 and round the
       result): bit for bit against torch on the CPU.
-    * ROCm torch's own fp16 `scalar * tensor` kernel rounds the exact product
-      once on its non-vectorised paths: every tie element of a tensor of at
-      most 256 elements and of a misaligned view differs from the CPU by one
-      unit, and so do the elements of an aligned tensor past its vectorised
-      part (512 of 2,560 were seen); the vectorised part of an aligned tensor
-      rounds twice like the CPU. The reference's expressions run by ROCm torch therefore
+    * ROCm torch's own fp16 `scalar * tensor` kernel is run on tensors made
+      only of tie values and compared with the CPU. On torch 2.10 / ROCm 7 it
+      rounded the exact product once on its non-vectorised paths: every tie
+      element of a tensor of at most 256 elements and of a misaligned view
+      differed from the CPU by one unit, and so did the elements of an aligned
+      tensor past its vectorised part (512 of 2,560); the vectorised part
+      rounded twice like the CPU. Those counts are printed, not asserted (they
+      are the torch build's, not the library's); the test asserts only that
+      where the two differ they are one unit apart, a difference of tie
+      rounding. The reference's expressions run by ROCm torch therefore
       differ from the reference (run on CUDA) on such ties, which is why the
       long runs compare against the CPU/CUDA recipe."""
     from dizo_amd.table import ZOTable
@@ -354,12 +358,16 @@ def test_update_rounds_ties_like_torch_cpu_and_cuda():
 
     # ROCm torch's kernel on tensors made only of tie values; lr * c is applied
     # to c itself (a view when off > 0: g * c would hand it a fresh aligned copy)
+    widest = 0
+
     def rocm_vs_cpu(n: int, off: int) -> int:
+        nonlocal widest
         vals = torch.from_numpy(rng_.choice(np.concatenate([ties, -ties]), size=n + off).astype(np.float16))
         dev = vals.cuda()[off:]
-        got = (lr * dev).cpu()
-        want = lr * vals[off:]
-        return int((got.view(torch.int16) != want.view(torch.int16)).sum())
+        got = (lr * dev).cpu().view(torch.int16).long()
+        want = (lr * vals[off:]).view(torch.int16).long()
+        widest = max(widest, int((got - want).abs().max()))
+        return int((got != want).sum())
 
     small = [rocm_vs_cpu(k, 0) for k in (1, 7, 64, 256)]
     misaligned = [rocm_vs_cpu(k, 1) for k in (2560, 65536)]
@@ -367,10 +375,7 @@ def test_update_rounds_ties_like_torch_cpu_and_cuda():
     body = rocm_vs_cpu(65536, 0)
     print(f"ROCm torch vs CPU on tie elements: n=1,7,64,256 -> {small}; misaligned 2560, 65536 -> {misaligned}; "
           f"aligned 2560 -> {tail}; aligned 65536 -> {body}", flush=True)
-    assert small == [1, 7, 64, 256]
-    assert misaligned == [2560, 65536]
-    assert 0 < tail < 2560
-    assert body == 0
+    assert widest <= 1, f"ROCm torch and the CPU differ by {widest} units on tie products"
 
 
 @pytest.mark.parametrize("prefetch", [False, True])
