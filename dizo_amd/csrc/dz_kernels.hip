@@ -140,6 +140,25 @@ struct RmwTraits {
 // per SIMD (up to 128 VGPRs per lane).
 constexpr int kRmwWavesPerEU = 4;
 
+// bf16 pair tables (restore + update, and with the next perturbation) hold
+// each entry's 16-bit halves xor-ed with their own index i: a z field
+// h = sign << 15 | i then turns entry i into its signed value with one xor
+// against h (i ^ i = 0 and the sign lands on bit 15, the value's sign), which
+// a word-selecting xor does for one operand of a packed word at a time
+// (xor_hi below). It takes the bf16 three-way pass from 171 to 151 VALU
+// instructions per 8-element group; for the single-value bf16 tables of
+// perturb and update it measured 0.6-1.8 % slower (HBM-bound passes, same
+// box, alternating builds), so they keep plain entries. fp16 applies the
+// signs as packed FMA factors.
+__host__ __device__ constexpr bool rmw_index_xor(int dt, int mode) {
+  return dt == DZ_BF16 && rmw_pair_mode(mode);
+}
+// What of a z field h is xor-ed into its table entry's halves.
+template <int DT, int MODE>
+__device__ __forceinline__ uint32_t field_xor(uint32_t h) {
+  return rmw_index_xor(DT, MODE) ? (h & 0xffffu) : (h & 0x8000u);
+}
+
 // Table entry for z = +Q_T[i] (qbits = bits of Q_T[i]).
 template <int DT, int MODE>
 __device__ __forceinline__ uint32_t table_entry(uint32_t qbits, const DzScalars& sc) {
@@ -189,13 +208,15 @@ __device__ __forceinline__ void store_table(typename RmwTraits<DT, MODE>::E* tab
 #pragma unroll
   for (int v = 0; v < TableSlices<DT>::kSlices; ++v) {
     uint32_t e[kPer];
+    const uint32_t i0 = (uint32_t)(v * kRmwThreads + threadIdx.x) * kPer;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const uint32_t w = t.q[v][kPer == 4 ? i : i >> 1];
       const uint32_t qb = kPer == 4 ? w : (i & 1 ? w >> 16 : w & 0xffffu);
       e[i] = table_entry<DT, MODE>(qb, sc);
+      if constexpr (rmw_index_xor(DT, MODE)) e[i] ^= (i0 + i) * 0x10001u;
     }
-    E* dst = tab + (size_t)(v * kRmwThreads + threadIdx.x) * kPer;
+    E* dst = tab + i0;
     if constexpr (sizeof(E) == 4) {
 #pragma unroll
       for (int h = 0; h < kPer / 4; ++h) {
@@ -262,6 +283,30 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
+// (half EH of e) ^ (half WH of w), placed in the high half over a zero low
+// half: the fp32 pattern of the bf16 value it holds. Two high halves are one
+// v_bitop3_b32 ((e ^ w) & 0xffff0000); the other forms are one word-selecting
+// (SDWA) xor: each source reads bits 0..15 or 16..31 zero-extended, and the
+// result's bits 0..15 are written to bits 16..31 with zeros below. (Written
+// as the instruction: from the shift-and-xor expression the compiler forms it
+// for only some of the uses.)
+template <int EH, int WH>
+__device__ __forceinline__ float xor_hi(uint32_t e, uint32_t w) {
+  uint32_t r;
+  if constexpr (EH == 1 && WH == 1)
+    r = (e ^ w) & 0xffff0000u;
+  else if constexpr (EH == 0 && WH == 0)
+    asm("v_xor_b32_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_0"
+        : "=v"(r) : "v"(e), "v"(w));
+  else if constexpr (EH == 0)
+    asm("v_xor_b32_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+        : "=v"(r) : "v"(e), "v"(w));
+  else
+    asm("v_xor_b32_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:WORD_0"
+        : "=v"(r) : "v"(e), "v"(w));
+  return __uint_as_float(r);
+}
+
 // R_T(a + b) for one 16-bit value.
 template <int DT>
 __device__ __forceinline__ uint32_t add_one(uint32_t a, uint32_t b) {
@@ -323,8 +368,9 @@ __device__ __forceinline__ Entries16 lookup_pair16(uint32_t w, uint32_t w2,
 }
 
 // The two elements' new values from their entries. A field's sign bit (bit
-// 15 of its half) negates its table value; once the two lanes' values are
-// packed, that is one xor with w & 0x80008000.
+// 15 of its half) negates its table value: for fp16, once the two lanes'
+// values are packed, one xor with w & 0x80008000 (or a +-1.0 factor); for
+// bf16 the xor_hi that takes each value to its fp32 pattern.
 // R(th + sg * v) lane by lane for sg = +-1.0 (fp16): the product is exact, so
 // the fused multiply-add rounds th +- v once, as the add of the negated value does.
 __device__ __forceinline__ uint32_t fma_sign_pair(uint32_t sg, uint32_t v, uint32_t th) {
@@ -351,30 +397,20 @@ __device__ __forceinline__ uint32_t combine_pair16(uint32_t th, uint32_t w, uint
   if constexpr (!rmw_pair_mode(MODE)) {
     return add_pair<DT>(th, (t.e0 | (t.e1 << 16)) ^ (w & 0x80008000u));
   } else {
-    // bf16 (the fp16 pair modes return above). entry = b | (-d) << 16 for a
-    // positive z. Each signed table value is taken straight to its fp32 bit
-    // pattern: the low-half value of element 0 as (e0 + s0) << 16 with s0 its
-    // sign at bit 15 (adding 0x8000 below bit 16 flips bit 15 whatever the
-    // carry), a high-half value as (e & 0xffff0000) ^ sign at bit 31, the
-    // low-half value of element 1 as (e1 << 16) + sign at bit 31. The three
-    // adds are the reference's fp32 adds, each rounded to bf16 (round_bf16_f
-    // for the first two, one packing conversion for the last).
-    const uint32_t s0 = w & 0x8000u, s0h = s0 << 16, s1 = w & 0x80000000u;
-    const float b0 = __uint_as_float((t.e0 + s0) << 16);
-    const float b1 = __uint_as_float((t.e1 << 16) + s1);
-    const float nd0 = __uint_as_float((t.e0 & 0xffff0000u) ^ s0h);
-    const float nd1 = __uint_as_float((t.e1 & 0xffff0000u) ^ s1);
-    float lo = round_bf16_f(bf16_lo_f(th) + b0);
-    float hi = round_bf16_f(bf16_hi_f(th) + b1);
+    // bf16 pairs: entry i = (b ^ i) | ((-d) ^ i) << 16 for a positive z. Each
+    // signed value comes out as its fp32 pattern from one xor_hi against the
+    // element's z half (element 0: bits 0..15 of w, element 1: bits 16..31).
+    // The three adds are the reference's fp32 adds, each rounded to bf16
+    // (round_bf16_f for the first two, one packing conversion for the last).
+    float lo = round_bf16_f(bf16_lo_f(th) + xor_hi<0, 0>(t.e0, w));
+    float hi = round_bf16_f(bf16_hi_f(th) + xor_hi<0, 1>(t.e1, w));
     if constexpr (MODE == kModeRestoreUpdatePerturb) {
-      lo = round_bf16_f(lo + nd0);
-      hi = round_bf16_f(hi + nd1);
+      lo = round_bf16_f(lo + xor_hi<1, 0>(t.e0, w));
+      hi = round_bf16_f(hi + xor_hi<1, 1>(t.e1, w));
       // the next step's +1 perturbation uses the same b (same scale and eps)
-      const float c0 = __uint_as_float((t.f0 + (w2 & 0x8000u)) << 16);
-      const float c1 = __uint_as_float((t.f1 << 16) + (w2 & 0x80000000u));
-      return pack_bf16(lo + c0, hi + c1);
+      return pack_bf16(lo + xor_hi<0, 0>(t.f0, w2), hi + xor_hi<0, 1>(t.f1, w2));
     } else {
-      return pack_bf16(lo + nd0, hi + nd1);
+      return pack_bf16(lo + xor_hi<1, 0>(t.e0, w), hi + xor_hi<1, 1>(t.e1, w));
     }
   }
 }
@@ -398,12 +434,12 @@ __device__ __forceinline__ uint32_t apply_one(uint32_t th, uint32_t h, uint32_t 
       return r;
     }
   } else if constexpr (!rmw_pair_mode(MODE)) {
-    return add_one<DT>(th, (uint32_t)tab[h & 0x7fffu] ^ (h & 0x8000u));
+    return add_one<DT>(th, (uint32_t)tab[h & 0x7fffu] ^ field_xor<DT, MODE>(h));
   } else {
-    const uint32_t e = tab[h & 0x7fffu] ^ ((h & 0x8000u) * 0x10001u);
+    const uint32_t e = tab[h & 0x7fffu] ^ (field_xor<DT, MODE>(h) * 0x10001u);
     uint32_t r = add_one<DT>(add_one<DT>(th, e & 0xffffu), e >> 16);
     if constexpr (MODE == kModeRestoreUpdatePerturb) {
-      r = add_one<DT>(r, (tab[h2 & 0x7fffu] ^ (h2 & 0x8000u)) & 0xffffu);
+      r = add_one<DT>(r, (tab[h2 & 0x7fffu] ^ field_xor<DT, MODE>(h2)) & 0xffffu);
     }
     return r;
   }

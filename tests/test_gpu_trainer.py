@@ -200,7 +200,8 @@ def test_dizo_first_order_event_matches_reference(dt):
     deep copy per iteration, torch.norm, the reference's loss, torch's fp32
     autograd), each run freely from gamma = 0.
 
-    The gammas agree within 5 % (the measured difference is printed): the
+    The gammas agree within 2 % (the measured difference is printed: 0.96 %
+    for fp16, about 1e-6 for bf16 and fp32): the
     alpha-gradient is a heavily cancelling sum, which the reference's autograd
     accumulates in fp32 in torch's order and the library in fp64, and Adam
     normalises each step, so summation rounding moves gamma by a fraction of a
@@ -232,7 +233,7 @@ def test_dizo_first_order_event_matches_reference(dt):
     g_ref, _ = R.dizo_fo_event(model_b, anchors, names, batches)
     rel = float(((g_lib - g_ref).abs() / g_ref.abs().clamp_min(1e-6)).max())
     print(f"{dt}: largest relative gamma difference against the reference's fp32 autograd: {rel:.3g}", flush=True)
-    assert torch.allclose(g_lib, g_ref, rtol=5e-2, atol=1e-4), f"gamma {g_lib} vs {g_ref}"
+    assert torch.allclose(g_lib, g_ref, rtol=2e-2, atol=1e-4), f"gamma {g_lib} vs {g_ref}"
 
     R.dizo_fo_apply(model_c, anchors, names, [g_lib[i:i + 1] for i in range(len(names))])
     pa, pc = dict(model_a.named_parameters()), dict(model_c.named_parameters())
