@@ -190,7 +190,8 @@ int32_t check_range(uint64_t p, uint64_t bytes, const char* what, int32_t i) {
 // memory the library never allocates at run time. Layout: the projection
 // kernel's work counters, the group -> first chunk index, the chunk
 // descriptors and the per-chunk partial sums, for at most kStaticMaxGroups
-// groups and kStaticMaxChunks chunks of kProjChunk elements (8.6 G elements).
+// groups and kStaticMaxChunks chunks of proj_chunk_elems(dtype) elements (8.6 G
+// elements of a 16-bit type, 2.1 G of fp32).
 // Each device holds its own copy, at its own address (see static_scratch).
 // ---------------------------------------------------------------------------
 namespace {
@@ -493,7 +494,7 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
   t->projection = anchor_ptrs != nullptr;
   t->n = n;
   t->dev = ds;
-  t->chunk_elems = t->projection ? (uint32_t)dz::kProjChunk : (uint32_t)dz::rmw_chunk_elems(dtype);
+  t->chunk_elems = t->projection ? (uint32_t)dz::proj_chunk_elems(dtype) : (uint32_t)dz::rmw_chunk_elems(dtype);
   const int es = elem_size(dtype);
   uint64_t z = 0;
   uint64_t total_tiles = 0;
@@ -704,14 +705,15 @@ int32_t dz_group_sumsq_static(const uint64_t* ptrs, const uint64_t* anchor_ptrs,
   int32_t rc = current_device(&dev);
   if (rc) return rc;
   const int es = elem_size(dtype);
+  const uint64_t cn = (uint64_t)dz::proj_chunk_elems(dtype);
   uint64_t total = 0;
   for (int32_t i = 0; i < n; ++i) {
     if (numels[i] < 0) return fail(DZ_ERR_INVALID, "negative numel for tensor " + std::to_string(i));
-    total += ((uint64_t)numels[i] + dz::kProjChunk - 1) / dz::kProjChunk;
+    total += ((uint64_t)numels[i] + cn - 1) / cn;
   }
   if (total > kStaticMaxChunks) {
     return fail(DZ_ERR_INVALID, "the tensors make " + std::to_string(total) + " chunks of " +
-                                    std::to_string(dz::kProjChunk) + " elements; at most " +
+                                    std::to_string(cn) + " elements; at most " +
                                     std::to_string(kStaticMaxChunks) + " fit the static scratch");
   }
   for (int32_t i = 0; i < n; ++i) {
@@ -747,13 +749,14 @@ int32_t dz_group_sumsq_static(const uint64_t* ptrs, const uint64_t* anchor_ptrs,
     b.total_groups = (uint32_t)n;
     b.total_chunks = (uint32_t)total;
     b.elem_size = es;
+    b.chunk_elems = (int32_t)cn;
     b.first = g0 == 0;
     for (uint32_t k = 0; k < b.ngroups; ++k) {
       b.ptr[k] = ptrs[g0 + k];
       b.anchor[k] = anchor_ptrs[g0 + k];
       b.numel[k] = numels[g0 + k];
       b.chunk_begin[k] = next;
-      next += (uint32_t)(((uint64_t)numels[g0 + k] + dz::kProjChunk - 1) / dz::kProjChunk);
+      next += (uint32_t)(((uint64_t)numels[g0 + k] + cn - 1) / cn);
     }
     hipError_t e = dz::launch_static_plan(b, chunks, group_begin, counters, st);
     if (e != hipSuccess) return hip_fail(e, "plan kernel launch");

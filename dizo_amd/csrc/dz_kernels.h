@@ -87,12 +87,18 @@ __host__ __device__ constexpr bool rmw_prefetch_mode(int dtype, int mode) {
 constexpr uint32_t kPrefetchMinTilesDefault = 0;
 
 // Projection kernel geometry: persistent 1024-thread workgroups, one per CU,
-// taking 32768-element chunks (64 KB of theta and 64 KB of theta0 in 16-bit
-// T): each thread 4 (16-bit T) or 8 (fp32) 16-byte vectors of each. Two
-// workgroups per CU streamed slower (6.49 against 6.76 TB/s for a bare
-// two-read-one-write kernel), as did smaller workgroups on one counter.
+// taking chunks of proj_chunk_elems(dtype) elements: 32768 for 16-bit T (64 KB
+// of theta and 64 KB of theta0, 4 16-byte vectors of each per thread), 8192
+// for fp32 (32 KB, 2 vectors). Two workgroups per CU streamed slower (6.49
+// against 6.76 TB/s for a bare two-read-one-write kernel), as did smaller
+// workgroups on one counter. fp32's only workload, OPT-125m, projects 57 MB
+// per stream: 432 chunks of 32768 left two thirds of the CUs with two chunks
+// and the rest with one. In its ZO step (same box, two alternating runs
+// each), apply / norm / reverse+norm took 46 / 36 / 47 us with 32768-element
+// chunks, 34 / 30 / 40 with 16384, 32 / 31 / 40 with 8192 and 31 / 37 / 44
+// with 4096.
 constexpr int kProjThreads = 1024;
-constexpr int kProjChunk = 32768;
+__host__ __device__ constexpr int proj_chunk_elems(int dtype) { return dtype == DZ_F32 ? 8192 : 32768; }
 // Groups whose alphas a projection workgroup keeps in LDS (16 KB of fp32);
 // beyond that each chunk reads its group's alpha from memory.
 constexpr int kProjAlphaLds = 4096;
@@ -157,7 +163,8 @@ struct StaticPlanBatch {
   uint32_t total_groups;
   uint32_t total_chunks;
   int32_t elem_size;
-  uint32_t first;  // the first batch also zeroes the work counters
+  int32_t chunk_elems;  // proj_chunk_elems(dtype)
+  uint32_t first;       // the first batch also zeroes the work counters
 };
 hipError_t launch_static_plan(const StaticPlanBatch& b, DzChunk* chunks, uint32_t* group_begin, uint32_t* counters,
                               hipStream_t st);

@@ -1122,15 +1122,16 @@ __device__ __forceinline__ double block_sum_f64(double x, double* red) {
 }
 
 // A chunk the vector path takes whole: full size and 16-byte aligned.
+template <int DT>
 __device__ __forceinline__ bool proj_full_chunk(const DzChunk& ch) {
-  return ch.n == (uint32_t)kProjChunk && (ch.meta & kDzMetaAligned) != 0u;
+  return ch.n == (uint32_t)proj_chunk_elems(DT) && (ch.meta & kDzMetaAligned) != 0u;
 }
 
 // Vector-memory operations a thread issues for a full chunk: its 16-byte
 // loads of theta and theta0, and its stores of theta (none for SUMSQ).
 template <int DT, int MODE>
 struct ProjChunkOps {
-  static constexpr int kVecs = kProjChunk / (kProjThreads * (16 / (int)sizeof(typename DT_<DT>::S)));
+  static constexpr int kVecs = proj_chunk_elems(DT) / (kProjThreads * (16 / (int)sizeof(typename DT_<DT>::S)));
   static constexpr int kAfterTicket = 2 * kVecs + (MODE == kProjSumsq ? 0 : kVecs);
 };
 
@@ -1144,7 +1145,7 @@ __device__ __forceinline__ void proj_chunk(const DzChunk& ch, float alpha, doubl
   char* tp = (char*)ch.ptr;
   const char* ap = (const char*)ch.aux;
   double acc = 0.0;
-  if (proj_full_chunk(ch)) {
+  if (proj_full_chunk<DT>(ch)) {
     constexpr int kVecsPerThread = ProjChunkOps<DT, MODE>::kVecs;
     // alpha in both 16-bit lanes (the ZO modes' alpha is a value of T)
     const uint32_t alpha2 = (kES == 2 && MODE != kProjApplyF32) ? DT_<DT>::from_f(alpha) * 0x10001u : 0u;
@@ -1272,7 +1273,7 @@ __global__ void __launch_bounds__(kProjThreads) proj_kernel(const DzChunk* __res
     // chunk issues at least kAfterTicket of them after the ticket; the
     // partial path waits for everything), and the barrier that ends the chunk
     // waits for LDS alone
-    if (proj_full_chunk(ch)) {
+    if (proj_full_chunk<DT>(ch)) {
       proj_chunk<DT, MODE>(ch, alpha, partials + c, red);
       if (threadIdx.x == 0) ticket_wait<ProjChunkOps<DT, MODE>::kAfterTicket>();
     } else {
@@ -1354,7 +1355,7 @@ __global__ void __launch_bounds__(kProjThreads) finalize_kernel(const double* __
 
 // Chunk descriptors of a projection launch planned on the device (the
 // table-free norm pass): block g writes group g's chunks, split as
-// dz_table_create splits them (kProjChunk elements, the last one shorter;
+// dz_table_create splits them (proj_chunk_elems(dtype) elements, the last one shorter;
 // aligned when theta and theta0 are 16-byte aligned), and its first chunk
 // index; the last batch also writes the end index of the last group. The
 // first batch zeroes the work counters the projection kernel takes chunks
@@ -1371,14 +1372,15 @@ __global__ void __launch_bounds__(256) static_plan_kernel(StaticPlanBatch b, DzC
   const uint64_t p = b.ptr[g], a = b.anchor[g];
   const int64_t ne = b.numel[g];
   const uint32_t meta = gi | ((p % 16 == 0 && a % 16 == 0) ? kDzMetaAligned : 0u);
-  const uint32_t nch = (uint32_t)((ne + kProjChunk - 1) / kProjChunk);
+  const int64_t cn = b.chunk_elems;
+  const uint32_t nch = (uint32_t)((ne + cn - 1) / cn);
   for (uint32_t k = threadIdx.x; k < nch; k += blockDim.x) {
-    const uint64_t s = (uint64_t)k * kProjChunk;
+    const uint64_t s = (uint64_t)k * (uint64_t)cn;
     DzChunk c;
     c.ptr = p + s * (uint64_t)b.elem_size;
     c.aux = a + s * (uint64_t)b.elem_size;
     c.zgroup = s;
-    c.n = (uint32_t)min((int64_t)kProjChunk, ne - (int64_t)s);
+    c.n = (uint32_t)min(cn, ne - (int64_t)s);
     c.meta = meta;
     chunks[b.chunk_begin[g] + k] = c;
   }

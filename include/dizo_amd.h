@@ -181,8 +181,9 @@ int32_t dz_init(int32_t device);
  * `dtype` each; the outputs are dz_group_sumsq's, bit for bit. Chunk
  * descriptors, partial sums and work counters live in a static device array
  * of the library (10.5 MB per device, held until the process ends): at most
- * 4096 groups and 262,144 chunks of 32,768 elements (8.6 G elements); larger
- * inputs return DZ_ERR_INVALID. Every call on one device shares that array,
+ * 4096 groups and 262,144 chunks of 32,768 elements of a 16-bit type (8.6 G
+ * elements) or of 8,192 fp32 elements (2.1 G); larger inputs return
+ * DZ_ERR_INVALID. Every call on one device shares that array,
  * so calls that overlap in time on one device race: order them on one
  * stream. After dz_init(device) a call allocates nothing; without it, the
  * first call on a device does dz_init's work itself. */

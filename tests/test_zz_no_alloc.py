@@ -87,12 +87,14 @@ def test_static_rejects_more_than_the_scratch_holds():
     numels = L.i64_array([8] * 4097)
     with pytest.raises(L.DzError, match="group count"):
         L.call("dz_group_sumsq_static", ptrs, anchors, numels, 4097, dtype_code(dt), None, None, None, None)
-    # 262,145 chunks: one 32,768-element chunk too many (a 16 GiB allocation is not needed to ask)
-    t = torch.empty(8, dtype=dt, device="cuda")
-    numels = L.i64_array([32768 * 262144 + 1])
-    with pytest.raises(L.DzError, match="fit the static scratch"):
-        L.call("dz_group_sumsq_static", L.u64_array([t.data_ptr()]), L.u64_array([t.data_ptr()]), numels, 1,
-               dtype_code(dt), None, None, None, None)
+    # 262,145 chunks: one chunk too many (32,768 elements of a 16-bit type, 8,192 of fp32; no
+    # allocation of that size is needed to ask)
+    for dt2, chunk in ((torch.float16, 32768), (torch.bfloat16, 32768), (torch.float32, 8192)):
+        t = torch.empty(8, dtype=dt2, device="cuda")
+        numels = L.i64_array([chunk * 262144 + 1])
+        with pytest.raises(L.DzError, match="fit the static scratch"):
+            L.call("dz_group_sumsq_static", L.u64_array([t.data_ptr()]), L.u64_array([t.data_ptr()]), numels, 1,
+                   dtype_code(dt2), None, None, None, None)
 
 
 _FRESH = textwrap.dedent("""
