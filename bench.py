@@ -174,7 +174,7 @@ def amortised(steps: int, elapsed: float, event_s, interval: int = 50):
 ZO_PASSES = ("perturb", "update", "restore_update", "restore_update_perturb")
 
 
-def amortised_passes(summ: dict, steps: int, events: int, P: int, interval: int = 50) -> dict:
+def amortised_passes(summ: dict, steps: int, events: int, P: int, pass_bytes: float, interval: int = 50) -> dict:
     """Library launches and bytes per ZO parameter per step with one DiZO
     event per `interval` steps, as `value` amortises the event's time.
 
@@ -184,18 +184,24 @@ def amortised_passes(summ: dict, steps: int, events: int, P: int, interval: int 
     update before it and the +1 perturbation after it are launches of their
     own); both are measured in the window per event and spread over
     `interval` steps. Without events the window's own per-step figures are
-    returned."""
+    returned. pass_bytes: the algorithmic bytes of one RMW launch (2 b P).
+    Replays of captured steps are not timed; without a timed steady pass the
+    ZO launches are counted from the step's structure instead: two per step
+    and one more per event (the restore + update before it), as the eager
+    step launches them."""
     zo = [v for k, v in summ.items() if k in ZO_PASSES]
     ev = [v for k, v in summ.items() if k not in ZO_PASSES]
-    zo_launches = sum(v["launches"] for v in zo)
-    zo_bytes = sum(v["bytes_per_launch"] * v["launches"] for v in zo)
+    if "restore_update_perturb" in summ or "perturb" in summ:
+        zo_launches = sum(v["launches"] for v in zo)
+        zo_bytes = sum(v["bytes_per_launch"] * v["launches"] for v in zo)
+    else:
+        zo_launches = 2 * steps + events
+        zo_bytes = zo_launches * pass_bytes
     if not events:
         return {"bytes_per_param_per_step": (zo_bytes + sum(v["bytes_per_launch"] * v["launches"] for v in ev))
                 / (steps * P),
                 "library_launches_per_step": (zo_launches + sum(v["launches"] for v in ev)) / steps,
                 "event_amortisation": None}
-    steady = summ.get("restore_update_perturb") or summ.get("perturb")
-    pass_bytes = steady["bytes_per_launch"]
     zo_extra_launches = (zo_launches - 2 * steps) / events
     zo_extra_bytes = (zo_bytes - 2 * steps * pass_bytes) / events
     ev_launches = sum(v["launches"] for v in ev) / events
@@ -671,7 +677,7 @@ def main(argv=None):
                         "launches_per_step": rmw_launches / a.steps},
             # every library pass, per ZO parameter and per step, with the DiZO
             # event amortised one per 50 steps as in `value` (amortised_passes)
-            **amortised_passes(summ, a.steps, r["events"], r["P"]),
+            **amortised_passes(summ, a.steps, r["events"], r["P"], 2 * r["elem_bytes"] * r["P"]),
         },
         "kernels": summ,
         "loss_first_last": [r["losses"][0], r["losses"][-1]] if r["losses"] else None,
