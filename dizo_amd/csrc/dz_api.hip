@@ -213,12 +213,16 @@ struct dz_table {
   bool projection = false;
   int32_t n = 0;
   uint32_t chunk_elems = 0;  // tile size (elements)
-  uint32_t nchunks = 0;
-  uint32_t nfull = 0;        // ZO tables: the full, aligned tiles come first (the prefetching loop runs them)
+  uint32_t nchunks = 0;      // ZO tables: full, aligned tiles first (the prefetching loop runs them)
   std::vector<uint64_t> ptrs, aux, zoff;
   std::vector<int64_t> numels;
   std::vector<uint32_t> group_begin;  // n + 1 chunk indices (projection tables)
   DzChunk* d_chunks = nullptr;
+  // ZO tables whose restore + update + next perturbation launches use another
+  // tile size (rmw_chunk_elems): their own tile list, else empty
+  uint32_t fused_elems = 0;
+  uint32_t fused_nchunks = 0;
+  DzChunk* d_fused_chunks = nullptr;
   uint32_t* d_group_begin = nullptr;
   double* d_partials = nullptr;
   uint32_t* d_counters = nullptr;  // work counters of the persistent RMW / projection kernels
@@ -263,6 +267,7 @@ int32_t check_table(const dz_table* t) {
 
 void free_table(dz_table* t) {
   if (t->d_chunks) (void)hipFree(t->d_chunks);
+  if (t->d_fused_chunks) (void)hipFree(t->d_fused_chunks);
   if (t->d_group_begin) (void)hipFree(t->d_group_begin);
   if (t->d_partials) (void)hipFree(t->d_partials);
   if (t->d_counters) (void)hipFree(t->d_counters);
@@ -299,10 +304,18 @@ int32_t rmw(dz_table* t, int mode, const dz::DzScalars& s, const dz::DzScalarPtr
   if (rc) return rc;
   const dz::LaunchEvents ev = take_timing(t);
   if (t->projection) return fail(DZ_ERR_INVALID, "perturb/update need a ZO table (created without anchors)");
-  const uint32_t ntiles = t->nchunks;
+  // the tile list whose tile size the launch's kernel takes
+  const uint32_t want = (uint32_t)dz::rmw_chunk_elems(t->dtype, mode);
+  const DzChunk* chunks = t->d_chunks;
+  uint32_t ntiles = t->nchunks;
+  if (want != t->chunk_elems) {
+    if (want != t->fused_elems) return fail(DZ_ERR_INVALID, "internal: no tile list for this launch");
+    chunks = t->d_fused_chunks;
+    ntiles = t->fused_nchunks;
+  }
   if (ntiles == 0) return record_unlaunched(ev, stream);
-  hipError_t e = dz::launch_rmw(t->dtype, mode, t->d_chunks, ntiles, rmw_grid(t, ntiles), t->dev->tab[t->dtype], s,
-                                p, t->d_counters, ntiles >= t->prefetch_min_tiles, (hipStream_t)stream, ev);
+  hipError_t e = dz::launch_rmw(t->dtype, mode, chunks, ntiles, rmw_grid(t, ntiles), t->dev->tab[t->dtype], s, p,
+                                t->d_counters, ntiles >= t->prefetch_min_tiles, (hipStream_t)stream, ev);
   if (e != hipSuccess) return hip_fail(e, "rmw kernel launch");
   return DZ_OK;
 }
@@ -494,7 +507,8 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
   t->projection = anchor_ptrs != nullptr;
   t->n = n;
   t->dev = ds;
-  t->chunk_elems = t->projection ? (uint32_t)dz::proj_chunk_elems(dtype) : (uint32_t)dz::rmw_chunk_elems(dtype);
+  t->chunk_elems = t->projection ? (uint32_t)dz::proj_chunk_elems(dtype)
+                                 : (uint32_t)dz::rmw_chunk_elems(dtype, dz::kModePerturb);
   const int es = elem_size(dtype);
   uint64_t z = 0;
   uint64_t total_tiles = 0;
@@ -541,8 +555,17 @@ int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const
   std::vector<DzChunk> chunks;
   build_chunks(t, t->chunk_elems, &chunks, t->projection ? &t->group_begin : nullptr);
   t->nchunks = (uint32_t)chunks.size();
-  if (!t->projection) t->nfull = full_tiles_first(&chunks, t->chunk_elems);
+  if (!t->projection) (void)full_tiles_first(&chunks, t->chunk_elems);
   hipError_t e = upload_chunks(chunks, &t->d_chunks);
+  const uint32_t fused = (uint32_t)dz::rmw_chunk_elems(dtype, dz::kModeRestoreUpdatePerturb);
+  if (e == hipSuccess && !t->projection && fused != t->chunk_elems) {
+    std::vector<DzChunk> fc;
+    build_chunks(t, fused, &fc, nullptr);
+    (void)full_tiles_first(&fc, fused);
+    t->fused_elems = fused;
+    t->fused_nchunks = (uint32_t)fc.size();
+    e = upload_chunks(fc, &t->d_fused_chunks);
+  }
   if (e == hipSuccess && t->projection) {
     // The finalize kernel always runs, so these exist even with no chunks.
     e = hipMalloc(&t->d_group_begin, t->group_begin.size() * sizeof(uint32_t));

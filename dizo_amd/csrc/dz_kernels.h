@@ -33,7 +33,7 @@ struct DzPtrArray {
 
 // Read-modify-write kernel geometry. A workgroup of 1024 threads takes one
 // tile at a time from the table's work counters; each thread owns
-// rmw_groups(dtype) groups of 8 elements per tile. Measured on the MI355X at
+// rmw_groups(dtype, mode) groups of 8 elements per tile. Measured on the MI355X at
 // OPT-13B size (643 tensors, fp16): 64 KB tiles (four groups per thread) and
 // one workgroup per CU stream best for every mode: perturb 6.4 TB/s against
 // 6.05 with 16 KB tiles and two workgroups per CU (which a 64 KB table would
@@ -41,11 +41,21 @@ struct DzPtrArray {
 // 7.96 ms with six groups per thread and spilled with eight. fp32 uses 32 KB
 // tiles (one group of 8 fp32 per thread): its only workload, OPT-125m (347 MB
 // of parameters, about 40 tiles per CU), runs a pass in 121 us that way
-// against 140 us with 64 KB tiles.
+// against 140 us with 64 KB tiles. The bf16 restore + update + next
+// perturbation pass (prefetching loop, ALU-bound) takes three groups per
+// thread (48 KB tiles): at OPT-30B 18.87-18.94 ms against 19.79-19.86 ms with
+// four and 19.57-19.62 with two (same box, alternating builds), where the
+// single-value bf16 passes take 19.3 ms with three and 17.6 with four, and
+// the fp16 three-way pass 8.07 ms with three against 7.60 with four. A table
+// whose three-way tile size differs keeps a second tile list for it.
 constexpr int kRmwThreads = 1024;
-__host__ __device__ constexpr int rmw_groups(int dtype) { return dtype == DZ_F32 ? 1 : 4; }
-// Elements per tile of an RMW launch (the table's chunk size).
-__host__ __device__ constexpr int rmw_chunk_elems(int dtype) { return kRmwThreads * rmw_groups(dtype) * 8; }
+__host__ __device__ constexpr int rmw_groups(int dtype, int mode) {
+  return dtype == DZ_F32 ? 1 : (dtype == DZ_BF16 && mode == kModeRestoreUpdatePerturb) ? 3 : 4;
+}
+// Elements per tile of an RMW launch (the size of the table's tile list it runs over).
+__host__ __device__ constexpr int rmw_chunk_elems(int dtype, int mode) {
+  return kRmwThreads * rmw_groups(dtype, mode) * 8;
+}
 
 // LDS bytes of the per-launch delta table of an RMW launch: 16-bit entries
 // for perturb/update of 16-bit T, 32-bit entries otherwise (fp32 deltas, or

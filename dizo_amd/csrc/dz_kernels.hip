@@ -132,8 +132,8 @@ template <int DT, int MODE>
 struct RmwTraits {
   static constexpr bool kWide = (DT == DZ_F32 || rmw_pair_mode(MODE));
   using E = typename std::conditional<kWide, uint32_t, uint16_t>::type;
-  static constexpr int kGroups = rmw_groups(DT);
-  static constexpr int kChunk = rmw_chunk_elems(DT);
+  static constexpr int kGroups = rmw_groups(DT, MODE);
+  static constexpr int kChunk = rmw_chunk_elems(DT, MODE);
   static constexpr bool kPrefetch = rmw_prefetch_mode(DT, MODE);
 };
 // Waves per SIMD of an RMW launch: one 1024-thread workgroup per CU, 4 waves
@@ -767,7 +767,7 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, const typename Rm
 // workgroups on every XCD; wave 0 keeps a ring in LDS (while tile k streams,
 // the index of tile k+3 is taken and the descriptor of tile k+2 is loaded,
 // with scalar loads) and a barrier ends each tile. The chunk list holds its
-// nfull full, aligned tiles first. The last workgroup to finish resets the
+// full, aligned tiles first. The last workgroup to finish resets the
 // counters for the next launch.
 //
 // Two tile loops: the plain loop (rmw_tiles) loads each tile when its turn
