@@ -80,9 +80,9 @@ constexpr int kCounterWords = (kDoneSlot + 1) * kCounterStride;
 // Tile loops of the RMW launches. The 16-bit restore + update + next
 // perturbation passes, whose ALU work per tile is the largest, run the
 // prefetching loop (rmw_tiles_prefetch: the next full tile's loads go out
-// half-way through each tile's work). Measured on the MI355X, same box,
-// alternating builds: OPT-13B fp16 7.86-7.90 -> 7.58-7.61 ms, OPT-30B bf16
-// 20.10-20.16 -> 19.83-19.95 ms. The single-Philox passes run the same on
+// once the tile's first group is stored). Measured on the MI355X, same box,
+// alternating builds, kernel microbench: OPT-13B fp16 7.86-7.90 -> 7.58-7.61
+// ms, OPT-30B bf16 20.10-20.16 -> 19.83-19.95 ms. The single-Philox passes run the same on
 // either loop (OPT-13B fp16 perturb 7.66-7.69 ms both, OPT-30B bf16 17.76 ms
 // both) and keep the plain loop (rmw_tiles), as does fp32.
 __host__ __device__ constexpr bool rmw_prefetch_mode(int dtype, int mode) {
@@ -91,7 +91,7 @@ __host__ __device__ constexpr bool rmw_prefetch_mode(int dtype, int mode) {
 // A table's default for the launches that use the prefetching loop: those of
 // at least this many tiles (dz_table_set_prefetch_min_tiles sets it per
 // table). 0: every launch of such a mode. With the next tile's loads issued
-// half-way, the prefetching loop is also the faster one for a short pass
+// inside the tile's work, the prefetching loop is also the faster one for a short pass
 // (OPT-2.7B fp16, 77 K tiles, in the ZO step: 1.544-1.545 against
 // 1.562-1.563 ms).
 constexpr uint32_t kPrefetchMinTilesDefault = 0;

@@ -630,16 +630,20 @@ __device__ __forceinline__ void apply_store_group32(uint64_t base, const TileOff
 // two ran one after the other (three-way pass at OPT-13B: 8.9 -> 8.2 ms at
 // equal Philox rounds).
 // kLoadNext (the prefetching tile loop): the next tile's loads, from nptr
-// into *nxt, go out once the first half of the groups are stored (for one
-// group per thread, before the Philox chains), held there by scheduling
-// barriers. Measured at OPT-13B fp16, three-way pass, same box, alternating
-// builds: 7.86-7.90 ms with the loads issued before the Philox chains,
-// 7.69-7.70 after them, 7.58-7.59 half-way, 7.60 three quarters in, and
-// 7.89 with one vector loaded after each group's store; OPT-30B bf16
-// 20.10-20.16 -> 19.83-19.89 ms half-way. Issued at the start, the next
-// tile's reads meet this tile's first stores in the memory system (rocprofv3
-// counts 18 % fewer reads in flight and 2.7 times the L2 tag stalls per
-// cycle of the perturb pass).
+// into *nxt, go out once the first group is stored (for one group per
+// thread, before the Philox chains), held there by scheduling barriers.
+// Measured at OPT-13B fp16, three-way pass, kernel microbench, same box,
+// alternating builds: 7.86-7.90 ms with the loads issued before the Philox
+// chains, 7.69-7.70 after them, 7.58-7.59 half-way, 7.59 a quarter in, 7.60
+// three quarters in, and 7.89 with one vector loaded after each group's
+// store; OPT-30B bf16 20.10-20.16 -> 19.83-19.89 ms half-way. In the ZO step
+// (the bench's 20-step command, three alternating runs each), where the pass
+// follows the GEMMs at a lower clock, after the first of four groups
+// 7.63-7.66 ms, half-way 7.73-7.78, three quarters in 7.68-7.72; with three
+// groups (bf16) after the first and after the second measured the same.
+// Issued at the start, the next tile's reads meet this tile's first stores in
+// the memory system (rocprofv3 counts 18 % fewer reads in flight and 2.7
+// times the L2 tag stalls per cycle of the perturb pass).
 template <int DT, int MODE, bool kUniformHi, bool kLoadNext = false>
 __device__ __forceinline__ void tile_body(const DzChunk& ch, const TileOffsets<DT, MODE>& to,
                                           const TileRegs<DT, MODE>& r,
@@ -647,7 +651,7 @@ __device__ __forceinline__ void tile_body(const DzChunk& ch, const TileOffsets<D
                                           uint64_t nptr = 0, TileRegs<DT, MODE>* nxt = nullptr) {
   constexpr int G = RmwTraits<DT, MODE>::kGroups;
   // the next tile's loads go out after group kLoadAfter's stores (-1: first)
-  constexpr int kLoadAfter = G > 1 ? G / 2 - 1 : -1;
+  constexpr int kLoadAfter = G > 1 ? 0 : -1;
   if constexpr (kLoadNext && kLoadAfter < 0) {
     load_tile_at<DT, MODE>(nptr, to, *nxt);
     __builtin_amdgcn_sched_barrier(0);
@@ -773,8 +777,8 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, const typename Rm
 // Two tile loops: the plain loop (rmw_tiles) loads each tile when its turn
 // comes; the prefetching loop (rmw_tiles_prefetch, the 16-bit restore +
 // update + next perturb passes; a table can set a minimum launch size,
-// dz_table_set_prefetch_min_tiles) issues the next full tile's loads
-// half-way through each tile's work, and hands the workgroup's remaining
+// dz_table_set_prefetch_min_tiles) issues the next full tile's loads once
+// each tile's first group is stored, and hands the workgroup's remaining
 // tiles to rmw_tiles at its first tile that is not full.
 // ---------------------------------------------------------------------------
 template <int DT, int MODE>
@@ -835,7 +839,7 @@ __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F7
 
 // One tile of the prefetching tile loop (see rmw_tiles_prefetch): full tile
 // k is computed from `cur` (loaded during tile k - 1) while tile k + 1 is
-// loaded into `nxt` (the loads go out half-way through, in tile_body).
+// loaded into `nxt` (the loads go out after the first group, in tile_body).
 // Returns whether tile k + 1 is a full tile (its data is then in `nxt`); if
 // it is not, the loads read a stand-in of the same size (the quantile
 // table), so that every path issues the same loads.
