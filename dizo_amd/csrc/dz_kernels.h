@@ -77,16 +77,19 @@ constexpr int kDoneSlot = kCounters;
 constexpr int kCounterStride = 32;  // uint32 slots (128 bytes)
 constexpr int kCounterWords = (kDoneSlot + 1) * kCounterStride;
 
-// Tile loops of the RMW launches. The 16-bit restore + update + next
-// perturbation passes, whose ALU work per tile is the largest, run the
-// prefetching loop (rmw_tiles_prefetch: the next full tile's loads go out
-// once the tile's first group is stored). Measured on the MI355X, same box,
-// alternating builds, kernel microbench: OPT-13B fp16 7.86-7.90 -> 7.58-7.61
-// ms, OPT-30B bf16 20.10-20.16 -> 19.83-19.95 ms. The single-Philox passes run the same on
-// either loop (OPT-13B fp16 perturb 7.66-7.69 ms both, OPT-30B bf16 17.76 ms
-// both) and keep the plain loop (rmw_tiles), as does fp32.
+// Tile loops of the RMW launches. The restore + update + next perturbation
+// passes, whose ALU work per tile is the largest, run the prefetching loop
+// (rmw_tiles_prefetch: the next full tile's loads go out once the tile's
+// first group is stored; with fp32's one group per thread, before the tile's
+// Philox chain). Measured on the MI355X, same box, alternating builds, kernel
+// microbench: OPT-13B fp16 7.86-7.90 -> 7.58-7.61 ms, OPT-30B bf16
+// 20.10-20.16 -> 19.83-19.95 ms, OPT-125m fp32 0.1220-0.1227 -> 0.1205-0.1207
+// ms (in the step 0.1216-0.1217 -> 0.1210-0.1211; with the loads issued after
+// the tile's store instead, 0.130 ms). The single-Philox passes run the same
+// on either loop (OPT-13B fp16 perturb 7.66-7.69 ms both, OPT-30B bf16
+// 17.76 ms both) and keep the plain loop (rmw_tiles).
 __host__ __device__ constexpr bool rmw_prefetch_mode(int dtype, int mode) {
-  return dtype != DZ_F32 && mode == kModeRestoreUpdatePerturb;
+  return mode == kModeRestoreUpdatePerturb;
 }
 // A table's default for the launches that use the prefetching loop: those of
 // at least this many tiles (dz_table_set_prefetch_min_tiles sets it per

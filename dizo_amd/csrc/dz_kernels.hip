@@ -775,8 +775,8 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, const typename Rm
 // counters for the next launch.
 //
 // Two tile loops: the plain loop (rmw_tiles) loads each tile when its turn
-// comes; the prefetching loop (rmw_tiles_prefetch, the 16-bit restore +
-// update + next perturb passes; a table can set a minimum launch size,
+// comes; the prefetching loop (rmw_tiles_prefetch, the restore + update +
+// next perturb passes; a table can set a minimum launch size,
 // dz_table_set_prefetch_min_tiles) issues the next full tile's loads once
 // each tile's first group is stored, and hands the workgroup's remaining
 // tiles to rmw_tiles at its first tile that is not full.

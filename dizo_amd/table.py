@@ -105,8 +105,8 @@ class _Table:
 
     def set_prefetch_min_tiles(self, min_tiles: int) -> None:
         """Launches of the fused restore+update+next perturb pass with at least
-        min_tiles tiles run the prefetching tile loop (16-bit tables; 0, the
-        default: every launch; 2**32 - 1: none). The computed values do not
+        min_tiles tiles run the prefetching tile loop (0, the default: every
+        launch; 2**32 - 1: none). The computed values do not
         depend on it."""
         L.call("dz_table_set_prefetch_min_tiles", self.handle, int(min_tiles))
 

@@ -68,7 +68,12 @@ int32_t dz_philox_host(uint64_t seed, uint32_t stream_id, uint64_t q, uint32_t o
  * projection table whose tensor i is group i with anchor theta0_i.
  * z_offsets (may be NULL) gives each tensor's global z index (a multiple of
  * 8); NULL lays the tensors end to end from 0, each rounded up to 8 elements.
- * Each address range is checked against its device allocation.
+ * Each address range is checked against its device allocation. The table
+ * holds device memory until dz_table_destroy: 32-byte tile descriptors (one
+ * per 32,768 elements of a 16-bit type or 8,192 fp32 elements; a bf16 ZO
+ * table also one per 24,576 elements for its restore + update + next
+ * perturbation launches; a projection table one per chunk and an fp64
+ * partial sum per chunk) and its work counters.
  * Replaces the trainable-set walk of trainer.py:1147-1160 (ZO table) and the
  * exclude_list walk of trainer.py:405-451, 581-584 (projection table). */
 int32_t dz_table_create(const uint64_t* ptrs, const uint64_t* anchor_ptrs, const int64_t* numels,
@@ -96,12 +101,12 @@ int32_t dz_table_z_offset(const dz_table* t, int32_t idx, uint64_t* out);
 int32_t dz_table_time_next(dz_table* t, void* start_event, void* stop_event);
 
 /* Tuning hook (no counterpart in the reference): the fused
- * restore+update+next perturb pass of a 16-bit table runs its prefetching
- * tile loop (the next tile loaded while the current one computes) only for
+ * restore+update+next perturb pass of a table runs its prefetching tile
+ * loop (the next tile loaded while the current one computes) only for
  * launches of at least min_tiles tiles; smaller launches run the plain loop.
  * The default, 0, selects it for every launch: measured on the MI355X in the
- * ZO step it is the faster loop at 77 K tiles (OPT-2.7B) and at 384 K
- * (OPT-13B). Tests set a large value to run the plain loop. The values the
+ * ZO step it is the faster loop at 10 K fp32 tiles (OPT-125m), 77 K fp16
+ * tiles (OPT-2.7B) and 384 K (OPT-13B). Tests set a large value to run the plain loop. The values the
  * passes compute do not depend on it. */
 int32_t dz_table_set_prefetch_min_tiles(dz_table* t, uint32_t min_tiles);
 
