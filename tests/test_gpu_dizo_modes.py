@@ -29,10 +29,10 @@ def _lib_norm(t: torch.Tensor) -> torch.Tensor:
     return torch.sqrt(s.double()).float().to(t.dtype)
 
 
-def _pair(dt, seed=13):
+def _pair(dt, seed=13, shape="opt-tiny"):
     """Two identical models moved away from their (identical) anchors, and the anchors."""
     from dizo_amd.synth import build_opt
-    model_a = build_opt("opt-tiny", dt, "cuda", seed=seed)
+    model_a = build_opt(shape, dt, "cuda", seed=seed)
     anchor = copy.deepcopy(model_a)
     gen = torch.Generator(device="cuda").manual_seed(seed)
     with torch.no_grad():
@@ -92,17 +92,16 @@ def test_supplied_gamma_matches_reference(dt):
     dz.close()
 
 
-@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
-def test_grid_search_matches_reference_procedure(dt):
-    """The searched ratio: for each of 8 ratios in [0.5, 1.0], the loss of a
-    deep copy with that ratio applied; the lowest wins and is applied. Same
-    losses, same choice, same weights as the library's in-place search."""
-    from dizo_amd.synth import make_batches
-    from dizo_amd.trainer import forward_wrap_with_option_len
-    model_a, model_b, anchor = _pair(dt, seed=15)
+def _grid_case(dt, shape, batch, seed):
+    """The searched ratio (ENHANCED=grid) on `shape`: for each of 8 ratios in
+    [0.5, 1.0] the reference procedure takes a deep copy, applies the ratio
+    to every projected tensor and evaluates the loss with the oracle's
+    restatement of the reference's forward wrap (trainer.py:470-542); the
+    lowest wins and is applied. The library's in-place search must give the
+    same losses, the same choice and the same weights, bit for bit."""
+    model_a, model_b, anchor = _pair(dt, seed=seed, shape=shape)
     dz = _dizo(anchor)
     names = dz.constraints_name
-    batch = make_batches(1, 4, 512, seed=9, device="cuda", min_len=8, max_len=20)[0]
     cands = tuple(np.linspace(0.5, 1.0, 8))
     model_a.eval()
     r, losses = dz.grid_search(model_a, anchor, batch, cands)
@@ -115,7 +114,7 @@ def test_grid_search_matches_reference_procedure(dt):
         with torch.no_grad():
             for n in names:
                 pm[n].copy_((pm[n] - p0[n]) * a + p0[n])
-            ref_losses.append(forward_wrap_with_option_len(m, **batch, return_dict=True).loss.float())
+            ref_losses.append(R.forward_wrap_with_option_len(m, **batch).float())
         del m
     assert all(_same(x, y.reshape(())) for x, y in zip(losses, ref_losses)), (losses, ref_losses)
     best = int(torch.stack(ref_losses).argmin())
@@ -128,6 +127,24 @@ def test_grid_search_matches_reference_procedure(dt):
     pa = dict(model_a.named_parameters())
     assert all(_same(pa[n].data, pb[n].data) for n in pa)
     dz.close()
+    return len(names), [float(x) for x in losses], r
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_grid_search_matches_reference_procedure(dt):
+    from dizo_amd.synth import make_batches
+    batch = make_batches(1, 4, 512, seed=9, device="cuda", min_len=8, max_len=20)[0]
+    _grid_case(dt, "opt-tiny", batch, 15)
+
+
+def test_c3_shape_grid_search_matches_reference_procedure():
+    """The grid event at config C3's shape (OPT-2.7B fp16, 64 k/v groups, one
+    batch of 16 x 2 candidates of length U[32, 64])."""
+    from dizo_amd.synth import make_batches
+    batch = make_batches(1, 16, 50272, seed=29, device="cuda", min_len=32, max_len=64)[0]
+    groups, losses, r = _grid_case(torch.float16, "opt-2.7b", batch, 17)
+    print(f"C3 grid: {groups} groups, losses {losses}, ratio {r}", flush=True)
+    assert groups == 64
 
 
 def test_c1_mezo_step_and_fixed_ratio_projection_match_cpu_oracle():

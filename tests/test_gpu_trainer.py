@@ -272,12 +272,20 @@ def test_dizo_first_order_iterations_within_the_fp32_sum_bound(dt):
     over the ten Adam steps (test_dizo_first_order_event_matches_reference):
     the sum cancels heavily and Adam normalises the step, so summation
     rounding moves gamma by a step's fraction."""
+    model_a, model_b, batches = _setup(dt, seed=23)
+    _fo_iterations_within_bound(model_a, model_b, batches, dt)
+
+
+def _fo_iterations_within_bound(model_a, model_b, batches, dt, noise_seed=4):
+    """The body of test_dizo_first_order_iterations_within_the_fp32_sum_bound
+    for two copies of one model: theta0 is model_a as given, theta = theta0 +
+    N(0, 1e-2) noise (the same on both copies); the library's dizo_trainer runs
+    on model_a, the oracle's procedure on model_b."""
     from dizo_amd.dizo import dizo_trainer
     from dizo_amd.synth import Cycle
     from dizo_amd.trainer import select_trainable
-    model_a, model_b, batches = _setup(dt, seed=23)
     anchor = copy.deepcopy(model_a)  # theta0; theta = theta0 + noise
-    gen = torch.Generator(device="cuda").manual_seed(4)
+    gen = torch.Generator(device="cuda").manual_seed(noise_seed)
     with torch.no_grad():
         for pa, pb in zip(model_a.parameters(), model_b.parameters()):
             noise = (torch.randn(pa.shape, device="cuda", generator=gen) * 1e-2).to(dt)
@@ -293,6 +301,8 @@ def test_dizo_first_order_iterations_within_the_fp32_sum_bound(dt):
     d_lib = _lib_group_norms([pa0[n].data for n in names], [anchors[n].data for n in names]).float()
     u = 2.0 ** -24
     worst = loosest = 0.0
+    big_groups = [0]
+    rel = [0.0]
     for it in range(10):
         data = dtr._next_batch()
         gamma_t = dz.gamma().detach().clone()
@@ -313,10 +323,25 @@ def test_dizo_first_order_iterations_within_the_fp32_sum_bound(dt):
             n_terms = prod.numel()
             d_ref = float(denoms[i])
             norm_term = abs(float(g_lib[i])) * abs(float(d_lib[i]) + 1e-8 - d_ref) / d_ref
-            bound = (n_terms * u * float(prod.abs().sum()) / (1 - n_terms * u)) / d_ref + norm_term \
-                + 4 * u * max(abs(float(g_lib[i])), abs(float(g_ref[i]))) + 1e-30
+            s_abs = float(prod.abs().sum())
+            tiny = 4 * u * max(abs(float(g_lib[i])), abs(float(g_ref[i]))) + 1e-30
             diff = abs(float(g_ref[i]) - float(g_lib[i]))
-            assert diff <= bound, f"iteration {it} group {i}: |{float(g_ref[i])} - {float(g_lib[i])}| > {bound}"
+            rel[0] = max(rel[0], diff / max(abs(float(g_ref[i])), 1e-30))
+            if n_terms * u <= 0.5:
+                # any fp32 summation order of n terms: gamma_n u sum|terms|
+                bound = n_terms * u * s_abs / (1 - n_terms * u) / d_ref + norm_term + tiny
+                assert diff <= bound, f"iteration {it} group {i}: |{float(g_ref[i])} - {float(g_lib[i])}| > {bound}"
+            else:
+                # gamma_n gives no fp32 bound once n u >= 1 (C4's groups: n u = 1.56). The
+                # library sums in fp64: its gradient against the fp64 sum of the reference's own
+                # terms, dL/dtheta' * Delta from the reference's autograd, is within two fp64
+                # any-order bounds (gamma_n with u = 2^-53), the norm term and rounding to fp32
+                u64 = 2.0 ** -53
+                g64 = float(prod.sum()) / d_ref + 1e-3 * float(torch.sign(gamma_t[i]))
+                bound = 2 * n_terms * u64 * s_abs / (1 - n_terms * u64) / d_ref + norm_term + tiny
+                diff = abs(float(g_lib[i]) - g64)
+                assert diff <= bound, f"iteration {it} group {i}: |{float(g_lib[i])} - {g64}| > {bound}"
+                big_groups[0] += 1
             worst = max(worst, diff / bound)
             loosest = max(loosest, bound / max(abs(float(g_lib[i])), 1e-30))
     dz(model_a, dtr.pre_trained, apply=True)  # trainer.py:830
@@ -327,8 +352,31 @@ def test_dizo_first_order_iterations_within_the_fp32_sum_bound(dt):
         d = _ulp_diff(pa[n].data, pb[n].data)
         assert int(d.max()) <= 1, f"{n}: {int(d.max())} ulp"
     print(f"largest gradient difference: {worst:.3g} of the bound; "
-          f"largest bound: {loosest:.3g} of the gradient", flush=True)
+          f"largest bound: {loosest:.3g} of the gradient ({big_groups[0]} group checks against the fp64 sum); "
+          f"largest relative difference from the reference's fp32 autograd gradient: {rel[0]:.3g}", flush=True)
     dtr.close()
+
+
+def test_c4_first_order_iterations_match_reference():
+    """ENHANCED=fo at the headline's scale (OPT-13B fp16: 80 k/v groups of
+    26,214,400 elements, batch 16 x 2 x 128): the ten iterations of the
+    first-order event against the oracle's restatement of the reference's
+    procedure, each from the library's gamma of that iteration: objective
+    within 1e-3, every group's gradient checked, and the final apply within
+    one unit in the last place. A group here has n = 26,214,400 terms, where
+    the fp32 bound for any summation order, gamma_n = n u / (1 - n u), does
+    not exist (n u = 1.56). The gradient is held instead against the fp64
+    sum of the reference's own per-element terms (dL/dtheta' * Delta from its
+    autograd) divided by its torch.norm: the library sums in fp64, so the two
+    differ by at most two fp64 any-order bounds (u = 2^-53: 5.8e-9 of
+    sum|terms| here), the norm term and fp32 rounding. Measured: 1.9e-9 of
+    sum|terms|, and the library's gradient within 7e-6 (relative) of the
+    reference's own fp32 autograd result (printed)."""
+    from dizo_amd.synth import build_opt, make_batches
+    model_a = build_opt("opt-13b", torch.float16, "cuda", seed=13)
+    model_b = copy.deepcopy(model_a)
+    batches = make_batches(4, 16, 50272, seed=19, device="cuda", fixed_len=128)
+    _fo_iterations_within_bound(model_a, model_b, batches, torch.float16)
 
 
 def _run_trainer(dt, graph, enhanced, steps, batches, seed=31, option_head=False, grads=None, **kw):
