@@ -459,6 +459,21 @@ __device__ __forceinline__ dz_u32x4 ld_stream(const void* p) {
 __device__ __forceinline__ void st_stream(void* p, dz_u32x4 v) {
   __builtin_nontemporal_store(v, (dz_global_u32x4*)(uintptr_t)p);
 }
+
+// Loads of a whole tile or chunk are buffer loads: the wave-uniform base
+// goes into a buffer descriptor on the scalar unit and each load takes the
+// thread's 32-bit offset (loop-invariant) as it is, where a global load of a
+// 64-bit address costs one v_lshl_add_u64 per vector (the compiler keeps
+// the offsets as 64-bit values, and a global load with a scalar base needs
+// them as 32-bit ones). The descriptor's range is the tile (`bytes`), its
+// fourth word the gfx9 raw-buffer format; cache policy 2 is the same
+// non-temporal hint as ld_stream's. Stores stay global stores.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(uint64_t base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)base, (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ dz_u32x4 ld_tile(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 2);
+}
 // Wave-uniform copy of a 32-bit value in a scalar register.
 // __builtin_amdgcn_readfirstlane returns a signed int: cast back to uint32_t
 // before widening, or values >= 2^31 would sign-extend.
@@ -580,10 +595,21 @@ struct TileOffsets {
   }
 };
 
-template <int DT, int MODE>
+// kBuf: buffer loads (ld_tile), for the prefetching loop, whose loads (of
+// the next tile) and stores (of this one) have different bases. The plain
+// loop's loads and stores share each vector's address, so there global
+// loads cost nothing extra; with buffer loads its single-value passes
+// measured 0.3-1 % slower.
+template <int DT, int MODE, bool kBuf = false>
 __device__ __forceinline__ void load_tile_at(uint64_t addr, const TileOffsets<DT, MODE>& to, TileRegs<DT, MODE>& r) {
+  if constexpr (kBuf) {
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(addr, RmwTraits<DT, MODE>::kChunk * DT_<DT>::kBits / 8);
 #pragma unroll
-  for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_stream((const char*)addr + to.at(i));
+    for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_tile(rs, (uint32_t)to.at(i));
+  } else {
+#pragma unroll
+    for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_stream((const char*)addr + to.at(i));
+  }
 }
 
 // Philox block of group threadIdx.x + u * 1024 of a tile: counter zgroup +
@@ -653,7 +679,7 @@ __device__ __forceinline__ void tile_body(const DzChunk& ch, const TileOffsets<D
   // the next tile's loads go out after group kLoadAfter's stores (-1: first)
   constexpr int kLoadAfter = G > 1 ? 0 : -1;
   if constexpr (kLoadNext && kLoadAfter < 0) {
-    load_tile_at<DT, MODE>(nptr, to, *nxt);
+    load_tile_at<DT, MODE, true>(nptr, to, *nxt);
     __builtin_amdgcn_sched_barrier(0);
   }
   constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
@@ -679,7 +705,7 @@ __device__ __forceinline__ void tile_body(const DzChunk& ch, const TileOffsets<D
     if constexpr (kLoadNext && kLoadAfter >= 0) {
       if (u == kLoadAfter) {
         __builtin_amdgcn_sched_barrier(0);
-        load_tile_at<DT, MODE>(nptr, to, *nxt);
+        load_tile_at<DT, MODE, true>(nptr, to, *nxt);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -838,20 +864,29 @@ __device__ __forceinline__ void rmw_tiles(uint32_t k0, const DzChunk* __restrict
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // One tile of the prefetching tile loop (see rmw_tiles_prefetch): full tile
-// k is computed from `cur` (loaded during tile k - 1) while tile k + 1 is
-// loaded into `nxt` (the loads go out after the first group, in tile_body).
-// Returns whether tile k + 1 is a full tile (its data is then in `nxt`); if
-// it is not, the loads read a stand-in of the same size (the quantile
-// table), so that every path issues the same loads.
+// k, whose descriptor `ch` the step before read, is computed from `cur`
+// (loaded during tile k - 1) while tile k + 1 is loaded into `nxt` (the loads
+// go out after the first group, in tile_body). Tile k + 1's descriptor is
+// read into `ch1`. Returns whether tile k + 1 is a full tile (its data is
+// then in `nxt`); if it is not, the loads read a stand-in of the same size
+// (the quantile table), so that every path issues the same loads.
+// Descriptor slot (k + 1) % 3 is next written in step k + 2, so the copy read
+// here is the one step k + 1 would read; carrying it saves each wave a
+// descriptor's LDS reads and its moves to scalar registers per tile. With
+// that, the bookkeeping below 64 KB of LDS (RmwShared), the wave test taken
+// once (wave0) and the next tile's buffer loads, a thread's VALU
+// instructions per tile of the three-way pass went from 459 to 448 for bf16
+// (three groups) and from 430 to 418 for fp16 (four groups).
 template <int DT, int MODE>
-__device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk* __restrict__ chunks, uint32_t nchunks,
+__device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk& ch, DzChunk& ch1,
+                                                  const DzChunk* __restrict__ chunks, uint32_t nchunks,
                                                   const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
                                                   const TileOffsets<DT, MODE>& to, uint32_t* sidx, DzChunk* sdesc,
                                                   uint32_t* mine, uint32_t ncnt, uint32_t j, const void* dummy,
-                                                  const TileRegs<DT, MODE>& cur, TileRegs<DT, MODE>& nxt) {
-  const DzChunk ch = uniform_chunk(sdesc[k % 3]);
+                                                  bool wave0, const TileRegs<DT, MODE>& cur,
+                                                  TileRegs<DT, MODE>& nxt) {
   const uint32_t c1 = rfl_u32(sidx[(k + 1) % 4]);
-  const DzChunk ch1 = uniform_chunk(sdesc[(k + 1) % 3]);
+  ch1 = uniform_chunk(sdesc[(k + 1) % 3]);
   const bool nxt_full = c1 < nchunks && full_tile<DT, MODE>(ch1) && tile_counters_share_high_word<DT, MODE>(ch1);
   const uint64_t nptr = nxt_full ? ch1.ptr : (uint64_t)(uintptr_t)dummy;
   // wave 0: the ticket of tile k + 3 and the descriptor of tile k + 2
@@ -859,7 +894,7 @@ __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk* __r
   uint64_t n_ptr = 0, n_zg = 0;
   uint32_t n_n = 0, n_meta = 0;
   bool have_desc = false;
-  if ((rfl_u32(threadIdx.x) >> 6) == 0) {  // wave 0 (uniform branch)
+  if (wave0) {  // uniform branch
     if (threadIdx.x == 0) grabbed = atomicAdd(mine, 1u);
     const uint32_t cd = rfl_u32(sidx[(k + 2) % 4]);
     if (cd < nchunks) {
@@ -912,15 +947,18 @@ __device__ __forceinline__ uint32_t rmw_tiles_prefetch(const DzChunk* __restrict
   // tile's size)
   static_assert(RmwTraits<DT, MODE>::kChunk <= kDzTabEntries, "the quantile table is a tile's stand-in");
   TileRegs<DT, MODE> a, b;
-  load_tile_at<DT, MODE>(ch0.ptr, to, a);
+  DzChunk da = ch0, db;
+  const bool wave0 = (rfl_u32(threadIdx.x) >> 6) == 0;
+  load_tile_at<DT, MODE, true>(ch0.ptr, to, a);
   uint32_t k = 0;
   for (;;) {
-    if (!rmw_prefetch_step<DT, MODE>(k, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j, dummy, a, b)) {
+    if (!rmw_prefetch_step<DT, MODE>(k, da, db, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j, dummy,
+                                     wave0, a, b)) {
       k += 1;
       break;
     }
-    if (!rmw_prefetch_step<DT, MODE>(k + 1, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j, dummy, b,
-                                     a)) {
+    if (!rmw_prefetch_step<DT, MODE>(k + 1, db, da, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j, dummy,
+                                     wave0, b, a)) {
       k += 2;
       break;
     }
@@ -929,6 +967,17 @@ __device__ __forceinline__ uint32_t rmw_tiles_prefetch(const DzChunk* __restrict
   wait_vm_all();  // the stand-in loads of the last step
   return k;
 }
+
+// The RMW kernel's LDS: the tile bookkeeping rings first, so that their
+// addresses stay below 64 KB and each wave's reads of them take one address
+// register and the DS instructions' 16-bit offset field (with the 128 KB
+// table first they took a register per read), then the launch's table.
+template <typename E>
+struct RmwShared {
+  DzChunk sdesc[3];      // descriptors of tiles k .. k + 2
+  uint32_t sidx[4];      // indices of tiles k .. k + 3
+  E tab[kDzTabEntries];  // the delta table
+};
 
 // kPF: run the prefetching tile loop over the workgroup's leading full tiles
 // (only where RmwTraits::kPrefetch allows it; the launcher picks it by size).
@@ -940,10 +989,10 @@ __global__ void __launch_bounds__(kRmwThreads, kRmwWavesPerEU) rmw_kernel(const 
                                                                           uint32_t* __restrict__ counters) {
   using Tr = RmwTraits<DT, MODE>;
   using E = typename Tr::E;
-  __shared__ __attribute__((aligned(16))) E tab[kDzTabEntries];
-  // Tile bookkeeping rings: indices of tiles k .. k+3, descriptors of k .. k+2.
-  __shared__ uint32_t sidx[4];
-  __shared__ DzChunk sdesc[3];
+  __shared__ __attribute__((aligned(16))) RmwShared<E> sh;
+  E* const tab = sh.tab;
+  uint32_t* const sidx = sh.sidx;
+  DzChunk* const sdesc = sh.sdesc;
   const DzScalars sc = resolve_scalars<DT>(sc_in, sp);
   // Counters in use: every one of them must be served by at least one
   // workgroup, or its tiles would never be taken (a small grid uses fewer).
@@ -1157,11 +1206,13 @@ __device__ __forceinline__ void proj_chunk(const DzChunk& ch, float alpha, doubl
                             ? recip_div(alpha)
                             : RecipDiv{0.0f, false};
     dz_u32x4 vt[kVecsPerThread], va[kVecsPerThread];
+    const __amdgpu_buffer_rsrc_t rt_ = tile_rsrc(ch.ptr, proj_chunk_elems(DT) * kES);
+    const __amdgpu_buffer_rsrc_t ra_ = tile_rsrc(ch.aux, proj_chunk_elems(DT) * kES);
 #pragma unroll
     for (int u = 0; u < kVecsPerThread; ++u) {
-      const size_t off = (size_t)(threadIdx.x + u * kProjThreads) * 16;
-      vt[u] = ld_stream(tp + off);
-      va[u] = ld_stream(ap + off);
+      const uint32_t off = (threadIdx.x + u * kProjThreads) * 16u;
+      vt[u] = ld_tile(rt_, off);
+      va[u] = ld_tile(ra_, off);
     }
 #pragma unroll
     for (int u = 0; u < kVecsPerThread; ++u) {
