@@ -460,20 +460,6 @@ __device__ __forceinline__ void st_stream(void* p, dz_u32x4 v) {
   __builtin_nontemporal_store(v, (dz_global_u32x4*)(uintptr_t)p);
 }
 
-// Loads of a whole tile or chunk are buffer loads: the wave-uniform base
-// goes into a buffer descriptor on the scalar unit and each load takes the
-// thread's 32-bit offset (loop-invariant) as it is, where a global load of a
-// 64-bit address costs one v_lshl_add_u64 per vector (the compiler keeps
-// the offsets as 64-bit values, and a global load with a scalar base needs
-// them as 32-bit ones). The descriptor's range is the tile (`bytes`), its
-// fourth word the gfx9 raw-buffer format; cache policy 2 is the same
-// non-temporal hint as ld_stream's. Stores stay global stores.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(uint64_t base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)base, (short)0, bytes, 0x00020000);
-}
-__device__ __forceinline__ dz_u32x4 ld_tile(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 2);
-}
 // Wave-uniform copy of a 32-bit value in a scalar register.
 // __builtin_amdgcn_readfirstlane returns a signed int: cast back to uint32_t
 // before widening, or values >= 2^31 would sign-extend.
@@ -595,21 +581,10 @@ struct TileOffsets {
   }
 };
 
-// kBuf: buffer loads (ld_tile), for the prefetching loop, whose loads (of
-// the next tile) and stores (of this one) have different bases. The plain
-// loop's loads and stores share each vector's address, so there global
-// loads cost nothing extra; with buffer loads its single-value passes
-// measured 0.3-1 % slower.
-template <int DT, int MODE, bool kBuf = false>
+template <int DT, int MODE>
 __device__ __forceinline__ void load_tile_at(uint64_t addr, const TileOffsets<DT, MODE>& to, TileRegs<DT, MODE>& r) {
-  if constexpr (kBuf) {
-    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(addr, RmwTraits<DT, MODE>::kChunk * DT_<DT>::kBits / 8);
 #pragma unroll
-    for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_tile(rs, (uint32_t)to.at(i));
-  } else {
-#pragma unroll
-    for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_stream((const char*)addr + to.at(i));
-  }
+  for (int i = 0; i < TileRegs<DT, MODE>::kVecs; ++i) r.v[i] = ld_stream((const char*)addr + to.at(i));
 }
 
 // Philox block of group threadIdx.x + u * 1024 of a tile: counter zgroup +
@@ -679,7 +654,7 @@ __device__ __forceinline__ void tile_body(const DzChunk& ch, const TileOffsets<D
   // the next tile's loads go out after group kLoadAfter's stores (-1: first)
   constexpr int kLoadAfter = G > 1 ? 0 : -1;
   if constexpr (kLoadNext && kLoadAfter < 0) {
-    load_tile_at<DT, MODE, true>(nptr, to, *nxt);
+    load_tile_at<DT, MODE>(nptr, to, *nxt);
     __builtin_amdgcn_sched_barrier(0);
   }
   constexpr bool kTwoSeeds = MODE == kModeRestoreUpdatePerturb;
@@ -705,7 +680,7 @@ __device__ __forceinline__ void tile_body(const DzChunk& ch, const TileOffsets<D
     if constexpr (kLoadNext && kLoadAfter >= 0) {
       if (u == kLoadAfter) {
         __builtin_amdgcn_sched_barrier(0);
-        load_tile_at<DT, MODE, true>(nptr, to, *nxt);
+        load_tile_at<DT, MODE>(nptr, to, *nxt);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -873,10 +848,12 @@ __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F7
 // Descriptor slot (k + 1) % 3 is next written in step k + 2, so the copy read
 // here is the one step k + 1 would read; carrying it saves each wave a
 // descriptor's LDS reads and its moves to scalar registers per tile. With
-// that, the bookkeeping below 64 KB of LDS (RmwShared), the wave test taken
-// once (wave0) and the next tile's buffer loads, a thread's VALU
-// instructions per tile of the three-way pass went from 459 to 448 for bf16
-// (three groups) and from 430 to 418 for fp16 (four groups).
+// that, the bookkeeping below 64 KB of LDS (RmwShared) and the wave test
+// taken once (wave0), a thread's VALU instructions per tile of the three-way
+// pass went from 459 to 451 for bf16 (three groups) and from 430 to 422 for
+// fp16 (four groups). Loading the next tile with buffer loads (a descriptor
+// on the scalar unit, 32-bit offsets: no 64-bit address add per vector) took
+// 3-4 more off and measured no faster; it is left out.
 template <int DT, int MODE>
 __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk& ch, DzChunk& ch1,
                                                   const DzChunk* __restrict__ chunks, uint32_t nchunks,
@@ -949,7 +926,7 @@ __device__ __forceinline__ uint32_t rmw_tiles_prefetch(const DzChunk* __restrict
   TileRegs<DT, MODE> a, b;
   DzChunk da = ch0, db;
   const bool wave0 = (rfl_u32(threadIdx.x) >> 6) == 0;
-  load_tile_at<DT, MODE, true>(ch0.ptr, to, a);
+  load_tile_at<DT, MODE>(ch0.ptr, to, a);
   uint32_t k = 0;
   for (;;) {
     if (!rmw_prefetch_step<DT, MODE>(k, da, db, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j, dummy,
@@ -1206,13 +1183,11 @@ __device__ __forceinline__ void proj_chunk(const DzChunk& ch, float alpha, doubl
                             ? recip_div(alpha)
                             : RecipDiv{0.0f, false};
     dz_u32x4 vt[kVecsPerThread], va[kVecsPerThread];
-    const __amdgpu_buffer_rsrc_t rt_ = tile_rsrc(ch.ptr, proj_chunk_elems(DT) * kES);
-    const __amdgpu_buffer_rsrc_t ra_ = tile_rsrc(ch.aux, proj_chunk_elems(DT) * kES);
 #pragma unroll
     for (int u = 0; u < kVecsPerThread; ++u) {
-      const uint32_t off = (threadIdx.x + u * kProjThreads) * 16u;
-      vt[u] = ld_tile(rt_, off);
-      va[u] = ld_tile(ra_, off);
+      const size_t off = (size_t)(threadIdx.x + u * kProjThreads) * 16;
+      vt[u] = ld_stream(tp + off);
+      va[u] = ld_stream(ap + off);
     }
 #pragma unroll
     for (int u = 0; u < kVecsPerThread; ++u) {

@@ -22,9 +22,7 @@ They also check that the library emits no buffer stores: a 16-byte buffer
 store with a register scalar offset read its data registers after the next
 VALU instruction had overwritten them on the MI355X (the compiler adds the
 wait state after a global store of more than 8 bytes, and not after that
-form), so full-tile stores are global stores; and that the buffer loads the
-prefetching loop and the projection use are 16-byte loads with the
-non-temporal hint.
+form), so full-tile stores are global stores.
 """
 import os
 import re
@@ -168,16 +166,6 @@ def test_every_ticket_has_a_wait_and_nothing_touches_its_register(asm):
 def test_no_buffer_stores(asm):
     stores = [l.strip() for l in asm.splitlines() if re.match(r"\s*buffer_store", l)]
     assert not stores, stores[:3]
-
-
-def test_buffer_loads_are_streaming(asm):
-    """The tile and chunk loads that go through buffer descriptors (ld_tile)
-    are 16-byte loads at a register offset that carry the same non-temporal
-    hint as the global loads they replace (cache policy 2 in the builtin)."""
-    loads = [l.strip() for l in asm.splitlines() if re.match(r"\s*buffer_load", l)]
-    assert loads, "no buffer loads: the prefetching loop and the projection use them"
-    bad = [l for l in loads if not (l.startswith("buffer_load_dwordx4 ") and " offen" in l and l.endswith(" nt"))]
-    assert not bad, bad[:3]
 
 
 def test_names_vgpr_parser():
