@@ -695,6 +695,38 @@ __device__ __forceinline__ bool tile_counters_share_high_word(const DzChunk& ch)
   return (uint32_t)ch.zgroup <= 0xffffffffu - (kSpan - 1u);
 }
 
+// Whether the prefetching tile loop can take a tile: a full tile whose
+// Philox counters share their high word.
+template <int DT, int MODE>
+__device__ __forceinline__ bool prefetchable_tile(const DzChunk& ch) {
+  return full_tile<DT, MODE>(ch) && tile_counters_share_high_word<DT, MODE>(ch);
+}
+
+// Take bit of the RMW kernel's LDS descriptor ring: the top bit of a slot's
+// Philox group (a group index is an element index / 8, so its top three bits
+// are always clear), set when the slot holds a valid tile that
+// prefetchable_tile accepts. bf16 launches that run the prefetching loop set
+// it (ring_tagged); every reader of their ring clears it.
+constexpr uint64_t kRingTake = 1ull << 63;
+
+// Whether the prefetching loop's ring carries take bits: bf16 only, whose
+// three-way pass is VALU-bound (1.4-1.9 % faster with them); the fp16 pass,
+// which is not, measured 0.1 % slower.
+__host__ __device__ constexpr bool ring_tagged(int dtype) { return dtype == DZ_BF16; }
+
+// The next tile's descriptor as the prefetching loop's steps read it from the
+// ring: the address and the Philox group with its take bit. n and meta are
+// not read (0 here): the loop's body does not use them.
+__device__ __forceinline__ DzChunk uniform_next_chunk(const DzChunk& c) {
+  DzChunk u;
+  u.ptr = rfl_u64(c.ptr);
+  u.aux = 0;
+  u.zgroup = rfl_u64(c.zgroup);
+  u.n = 0;
+  u.meta = 0;
+  return u;
+}
+
 // Applies the launch's operation to a thread's share of a full tile, already
 // in registers, and stores it.
 template <int DT, int MODE>
@@ -782,7 +814,7 @@ __device__ __forceinline__ void rmw_partial(const DzChunk& ch, const typename Rm
 // each tile's first group is stored, and hands the workgroup's remaining
 // tiles to rmw_tiles at its first tile that is not full.
 // ---------------------------------------------------------------------------
-template <int DT, int MODE>
+template <int DT, int MODE, bool kTagged = false>
 __device__ __forceinline__ void rmw_tiles(uint32_t k0, const DzChunk* __restrict__ chunks, uint32_t nchunks,
                                           const typename RmwTraits<DT, MODE>::E* tab, const DzScalars& sc,
                                           const TileOffsets<DT, MODE>& to, uint32_t* sidx, DzChunk* sdesc,
@@ -792,7 +824,8 @@ __device__ __forceinline__ void rmw_tiles(uint32_t k0, const DzChunk* __restrict
   for (uint32_t k = k0;; ++k) {
     const uint32_t c = sidx[k % 4];
     if (c >= nchunks) break;
-    const DzChunk ch = uniform_chunk(sdesc[k % 3]);
+    DzChunk ch = uniform_chunk(sdesc[k % 3]);
+    if constexpr (kTagged) ch.zgroup &= ~kRingTake;
     // Wave 0 fetches a descriptor with scalar loads (it is uniform, so it
     // costs no vector registers); lane 0 takes an index with a vector
     // atomic. The anchor field is unused by ZO tables.
@@ -847,11 +880,15 @@ __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F7
 // (the quantile table), so that every path issues the same loads.
 // Descriptor slot (k + 1) % 3 is next written in step k + 2, so the copy read
 // here is the one step k + 1 would read; carrying it saves each wave a
-// descriptor's LDS reads and its moves to scalar registers per tile. With
-// that, the bookkeeping below 64 KB of LDS (RmwShared) and the wave test
-// taken once (wave0), a thread's VALU instructions per tile of the three-way
-// pass went from 459 to 451 for bf16 (three groups) and from 430 to 422 for
-// fp16 (four groups). Loading the next tile with buffer loads (a descriptor
+// descriptor's LDS reads and its moves to scalar registers per tile. For
+// bf16 (ring_tagged), wave 0, which writes the slot, also stores there
+// whether the loop can take the tile (kRingTake), so the other waves read
+// only the address and the Philox group (one ds_read2_b64, four lane moves;
+// no index, n or meta). With these, the bookkeeping below 64 KB of LDS
+// (RmwShared) and the wave test taken once (wave0), a thread's VALU
+// instructions per tile of the three-way pass went from 459 to 447 for bf16
+// (three groups; 2 more on every other step of the unrolled loop) and from
+// 430 to 422 for fp16 (four groups). Loading the next tile with buffer loads (a descriptor
 // on the scalar unit, 32-bit offsets: no 64-bit address add per vector) took
 // 3-4 more off and measured no faster; it is left out. So is reading tile
 // k + 1's descriptor from the table with scalar loads in every wave (wave 0
@@ -868,9 +905,23 @@ __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk& ch,
                                                   uint32_t* mine, uint32_t ncnt, uint32_t j, const void* dummy,
                                                   bool wave0, const TileRegs<DT, MODE>& cur,
                                                   TileRegs<DT, MODE>& nxt) {
-  const uint32_t c1 = rfl_u32(sidx[(k + 1) % 4]);
-  ch1 = uniform_chunk(sdesc[(k + 1) % 3]);
-  const bool nxt_full = c1 < nchunks && full_tile<DT, MODE>(ch1) && tile_counters_share_high_word<DT, MODE>(ch1);
+  bool nxt_full;
+  if constexpr (ring_tagged(DT)) {
+    // The slot's offset is opaque to the compiler, so both fields are read
+    // through one address register (one ds_read2_b64), and the take bit is
+    // tested on the high word (no 64-bit scalar compare).
+    uint32_t slot = (k + 1) % 3 * (uint32_t)sizeof(DzChunk);
+    asm("" : "+s"(slot));
+    ch1 = uniform_next_chunk(*(const DzChunk*)((const char*)sdesc + slot));
+    uint32_t zhi = (uint32_t)(ch1.zgroup >> 32);
+    asm("" : "+s"(zhi));  // keeps the test on 32 bits (no 64-bit compare folded back)
+    nxt_full = (int32_t)zhi < 0;
+    ch1.zgroup = (uint64_t)(zhi & 0x7fffffffu) << 32 | (uint32_t)ch1.zgroup;
+  } else {
+    const uint32_t c1 = rfl_u32(sidx[(k + 1) % 4]);
+    ch1 = uniform_chunk(sdesc[(k + 1) % 3]);
+    nxt_full = c1 < nchunks && prefetchable_tile<DT, MODE>(ch1);
+  }
   const uint64_t nptr = nxt_full ? ch1.ptr : (uint64_t)(uintptr_t)dummy;
   // wave 0: the ticket of tile k + 3 and the descriptor of tile k + 2
   uint32_t grabbed = 0;
@@ -887,6 +938,8 @@ __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk& ch,
       n_n = src->n;
       n_meta = src->meta;
       have_desc = true;
+      if constexpr (ring_tagged(DT))
+        if (prefetchable_tile<DT, MODE>(DzChunk{n_ptr, 0, n_zg, n_n, n_meta})) n_zg |= kRingTake;
     }
   }
   tile_body<DT, MODE, true, true>(ch, to, cur, tab, sc, nptr, &nxt);
@@ -895,14 +948,16 @@ __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk& ch,
   // loads issued behind it (vmcnt(2 * kVecs)) instead of draining them.
   if (threadIdx.x == 0) {
     sidx[(k + 3) % 4] = (uint32_t)min((uint64_t)grabbed * ncnt + j, (uint64_t)nchunks);
+    DzChunk& d = sdesc[(k + 2) % 3];
     if (have_desc) {
-      DzChunk& d = sdesc[(k + 2) % 3];
       d.ptr = n_ptr;
       d.aux = 0;
-      d.zgroup = n_zg;
+      if constexpr (!ring_tagged(DT)) d.zgroup = n_zg;
       d.n = n_n;
       d.meta = n_meta;
     }
+    // with the take bit step k + 1 reads; 0 (no take bit) past the table's end
+    if constexpr (ring_tagged(DT)) d.zgroup = n_zg;
   }
   lds_barrier();
   return nxt_full;
@@ -924,8 +979,9 @@ __device__ __forceinline__ uint32_t rmw_tiles_prefetch(const DzChunk* __restrict
                                                        uint32_t* sidx, DzChunk* sdesc, uint32_t* mine, uint32_t ncnt,
                                                        uint32_t j, const void* dummy) {
   const uint32_t c0 = rfl_u32(sidx[0]);
-  const DzChunk ch0 = uniform_chunk(sdesc[0]);
-  if (!(c0 < nchunks && full_tile<DT, MODE>(ch0) && tile_counters_share_high_word<DT, MODE>(ch0))) return 0;
+  DzChunk ch0 = uniform_chunk(sdesc[0]);
+  if constexpr (ring_tagged(DT)) ch0.zgroup &= ~kRingTake;
+  if (!(c0 < nchunks && prefetchable_tile<DT, MODE>(ch0))) return 0;
   // the stand-in must hold a whole tile (a thread's last vector ends at the
   // tile's size)
   static_assert(RmwTraits<DT, MODE>::kChunk <= kDzTabEntries, "the quantile table is a tile's stand-in");
@@ -1002,6 +1058,10 @@ __global__ void __launch_bounds__(kRmwThreads, kRmwWavesPerEU) rmw_kernel(const 
       const DzChunk d1 = chunks[min(c[1], nch - 1)];
       sdesc[0] = d0;
       sdesc[1] = d1;
+      if constexpr (Tr::kPrefetch && kPF && ring_tagged(DT)) {  // the take bits (kRingTake)
+        if (c[0] < nch && prefetchable_tile<DT, MODE>(d0)) sdesc[0].zgroup |= kRingTake;
+        if (c[1] < nch && prefetchable_tile<DT, MODE>(d1)) sdesc[1].zgroup |= kRingTake;
+      }
     }
   }
   store_table<DT, MODE>(tab, qs, sc);
@@ -1010,7 +1070,7 @@ __global__ void __launch_bounds__(kRmwThreads, kRmwWavesPerEU) rmw_kernel(const 
   uint32_t k0 = 0;
   if constexpr (Tr::kPrefetch && kPF)
     k0 = rmw_tiles_prefetch<DT, MODE>(chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j, qtab);
-  rmw_tiles<DT, MODE>(k0, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j);
+  rmw_tiles<DT, MODE, Tr::kPrefetch && kPF && ring_tagged(DT)>(k0, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j);
   if (threadIdx.x == 0) {
     const uint32_t done = atomicAdd(counters + kDoneSlot * kCounterStride, 1u);
     if (done == gridDim.x - 1) {
