@@ -888,15 +888,16 @@ __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F7
 // (RmwShared) and the wave test taken once (wave0), a thread's VALU
 // instructions per tile of the three-way pass went from 459 to 447 for bf16
 // (three groups; 2 more on every other step of the unrolled loop) and from
-// 430 to 422 for fp16 (four groups). Loading the next tile with buffer loads (a descriptor
-// on the scalar unit, 32-bit offsets: no 64-bit address add per vector) took
-// 3-4 more off and measured no faster; it is left out. So is reading tile
-// k + 1's descriptor from the table with scalar loads in every wave (wave 0
-// has read the entry a step earlier, so they hit the scalar cache): 7 fewer
-// per bf16 tile (149 per group counted), but each tile's start then waits
-// for the scalar loads, and the bf16 pass measured 1.4 % faster on one box
-// and 2-3 % slower on two others, also with the next index carried from the
-// step before so that those loads go out with no LDS read ahead of them.
+// 430 to 422 for fp16 (four groups). Loading the next tile with buffer loads
+// (a descriptor on the scalar unit, 32-bit offsets: no 64-bit address add per
+// vector) took 3-4 more off and measured no faster; it is left out. So is
+// reading tile k + 1's descriptor from the table with scalar loads in every
+// wave (wave 0 has read the entry a step earlier, so they hit the scalar
+// cache): 7 fewer per bf16 tile than without take bits (149 per group
+// counted), but each tile's start then waits for the scalar loads, and the
+// bf16 pass measured 1.4 % faster on one box and 2-3 % slower on two others,
+// also with the next index carried from the step before so that those loads
+// go out with no LDS read ahead of them.
 template <int DT, int MODE>
 __device__ __forceinline__ bool rmw_prefetch_step(uint32_t k, const DzChunk& ch, DzChunk& ch1,
                                                   const DzChunk* __restrict__ chunks, uint32_t nchunks,
@@ -1070,7 +1071,8 @@ __global__ void __launch_bounds__(kRmwThreads, kRmwWavesPerEU) rmw_kernel(const 
   uint32_t k0 = 0;
   if constexpr (Tr::kPrefetch && kPF)
     k0 = rmw_tiles_prefetch<DT, MODE>(chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j, qtab);
-  rmw_tiles<DT, MODE, Tr::kPrefetch && kPF && ring_tagged(DT)>(k0, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j);
+  constexpr bool kTagged = Tr::kPrefetch && kPF && ring_tagged(DT);  // the ring may hold take bits
+  rmw_tiles<DT, MODE, kTagged>(k0, chunks, nchunks, tab, sc, to, sidx, sdesc, mine, ncnt, j);
   if (threadIdx.x == 0) {
     const uint32_t done = atomicAdd(counters + kDoneSlot * kCounterStride, 1u);
     if (done == gridDim.x - 1) {
