@@ -554,6 +554,25 @@ def kernel_microbench(wl_name: str, reps: int = 10, log=print):
     t = float(np.median(ms))
     out["device_copy_4GiB"] = {"ms": t, "GBps": 2 * copy_bytes / t / 1e6, "frac": 2 * copy_bytes / t / 1e6 / HBM_PEAK_GBPS}
     log(f"[kernels] device copy 4 GiB {t:8.3f} ms {2 * copy_bytes / t / 1e6:8.1f} GB/s")
+    del src, dst
+    # context: PyTorch's own in-place elementwise kernel over 16 GiB (x ^= 0 on int32: every byte read and
+    # written once, the RMW passes' traffic pattern with no arithmetic), a practical streaming ceiling
+    ip_bytes = 16 << 30
+    buf = torch.zeros(ip_bytes // 4, dtype=torch.int32, device="cuda")
+    buf.bitwise_xor_(0)
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        buf.bitwise_xor_(0)
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    del buf
+    t = float(np.median(ms))
+    out["torch_inplace_16GiB"] = {"ms": t, "GBps": 2 * ip_bytes / t / 1e6, "frac": 2 * ip_bytes / t / 1e6 / HBM_PEAK_GBPS}
+    log(f"[kernels] torch in-place xor 16 GiB {t:8.3f} ms {2 * ip_bytes / t / 1e6:8.1f} GB/s")
     eb = torch.finfo(dtype).bits // 8
     # one ZO step of the reference (trainer.py:1580-1608): +1, -2, +1 and the update, 4 read-modify-write
     # passes; fused: +1, -2 and restore+update (3); across steps: -2 and restore+update+next perturb (2)
